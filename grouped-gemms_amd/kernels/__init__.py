@@ -1,0 +1,24 @@
+"""MI355X (gfx950) MX-scaled grouped-GEMM kernels, hand-written HIP behind a C ABI.
+
+Drop-in for the reference package ``kernels`` (kernels/__init__.py:17-25):
+
+  - ``triton_mxfp8_grouped_mm``: forward + dgrad grouped GEMM (A @ B^T per group)
+  - ``triton_mxfp8_wgrad``: weight-gradient grouped GEMM (A^T @ B per group)
+  - ``_rocm_mxfp8_available``: True when the native library is loadable on ROCm
+
+plus the on-GPU quantizers ``to_mx`` / ``to_mx_dim0`` (the reference quantizes
+with eager torch ops in utils.py:67-105).
+"""
+
+from ._common import _rocm_mxfp8_available
+from .backward import triton_mxfp8_wgrad
+from .forward import triton_mxfp8_grouped_mm
+from .quant import to_mx, to_mx_dim0
+
+__all__ = [
+    "triton_mxfp8_grouped_mm",
+    "triton_mxfp8_wgrad",
+    "_rocm_mxfp8_available",
+    "to_mx",
+    "to_mx_dim0",
+]

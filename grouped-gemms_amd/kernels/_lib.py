@@ -1,0 +1,109 @@
+"""ctypes binding of libmxgg.so (the C ABI declared in include/mxgg.h).
+
+The library is built in-tree next to this file (``make -C grouped-gemms_amd/csrc``
+or ``__graft_entry__.build()``).  There is no fallback: when the library is
+missing every operator raises ``NotImplementedError``, like the reference's
+stubs when its kernels are unavailable (kernels/forward.py:608-612).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmxgg.so")
+
+# status codes / enums (include/mxgg.h)
+OK = 0
+ERR_INVALID_ARG = -1
+ERR_UNSUPPORTED = -2
+ERR_WORKSPACE = -3
+ERR_NO_DEVICE = -4
+FMT_E4M3 = 0
+FMT_E2M1 = 4
+DTYPE_BF16 = 0
+DTYPE_F16 = 1
+DTYPE_F32 = 2
+
+_c_i32 = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_c_sz = ctypes.c_size_t
+_c_p = ctypes.c_void_p
+
+# (name, restype, argtypes) for every symbol of include/mxgg.h
+SIGNATURES = {
+    "mxgg_version": (_c_i32, []),
+    "mxgg_last_error_string": (ctypes.c_char_p, []),
+    "mxgg_device_supported": (_c_i32, []),
+    "mxgg_quantize_mx": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64,
+                                  _c_p, _c_i64, _c_p]),
+    "mxgg_quantize_mx_dim0": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64,
+                                       _c_p, _c_i64, _c_p]),
+    "mxgg_routing_words": (_c_i64, [_c_i32, _c_i64, _c_i32]),
+    "mxgg_build_routing": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_p, _c_p]),
+    "mxgg_schedule_programs": (_c_i64, [_c_i32, _c_i64, _c_i64, _c_i32, _c_i32]),
+    "mxgg_tile_schedule": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
+                                    _c_p, _c_p]),
+    "mxgg_grouped_mm": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
+                                 _c_p, _c_i32, _c_i64, _c_i64,
+                                 _c_p, _c_i64, _c_i64,
+                                 _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
+                                 _c_p, _c_i32, _c_i64,
+                                 _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
+    "mxgg_wgrad_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
+    "mxgg_wgrad": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
+                            _c_p, _c_i64, _c_p, _c_i64,
+                            _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
+                            _c_p, _c_i32, _c_p, _c_sz, _c_p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+_load_error: str | None = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and return the library with typed entry points."""
+    global _lib, _load_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            _load_error = f"{path} not built (run make -C grouped-gemms_amd/csrc)"
+            raise NotImplementedError(_load_error)
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except (NotImplementedError, OSError):
+        return False
+
+
+class MXGGError(RuntimeError):
+    """A libmxgg entry point returned a nonzero status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"libmxgg error {code}: {msg}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = load().mxgg_last_error_string().decode(errors="replace")
+    if rc == ERR_INVALID_ARG:
+        raise ValueError(msg)
+    if rc == ERR_NO_DEVICE:
+        raise NotImplementedError(msg)
+    raise MXGGError(rc, msg)

@@ -1,0 +1,78 @@
+"""Weight-gradient MX grouped GEMM on gfx950: ``triton_mxfp8_wgrad``.
+
+Drop-in for kernels/backward.py:217-305 of the reference:
+``grad_W[g] = grad_output[group_g]^T @ input_act[group_g]`` computed from the
+dim-1 quantized operands ``go_t (N, M)`` and ``ia_t (K, M)`` (scales per 32
+tokens), one reduction over each group's token range, output ``(E, N, K)``.
+As in the reference the stored values are rounded to bf16 whatever
+``out_dtype`` is (backward.py:103, 214) and an empty group yields zeros.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import _offsets, _out_code, _require, _rowmajor, _stream_handle, _u8
+
+
+def triton_mxfp8_wgrad(
+    go_t: torch.Tensor,
+    go_scale: torch.Tensor,
+    ia_t: torch.Tensor,
+    ia_scale: torch.Tensor,
+    group_end_offsets: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    BLOCK_N: int = 256,
+    BLOCK_K: int = 256,
+    BLOCK_M: int = 64,
+    num_warps: int = 8,
+    num_stages: int = 2,
+) -> torch.Tensor:
+    """MX weight gradient: ``grad_W[g] = grad_output[group_g]^T @ input_act[group_g]``.
+
+    Args (kernels/backward.py:238-243):
+        go_t: ``(N, M)`` float8_e4m3fn, grad_output quantized along M.
+        go_scale: ``(N, M//32)`` e8m0.
+        ia_t: ``(K, M)`` float8_e4m3fn, input activations quantized along M.
+        ia_scale: ``(K, M//32)`` e8m0.
+        group_end_offsets: ``(E,)`` int32 cumulative token counts, multiples of 32.
+        BLOCK_N / BLOCK_K / BLOCK_M / num_warps / num_stages: accepted for
+            signature compatibility; the HIP kernel uses its own tiling.
+
+    Returns ``(E, N, K)`` of ``out_dtype`` (bf16 or float32).
+    """
+    _require(go_t, "go_t")
+    N, M = go_t.shape
+    K, M2 = ia_t.shape
+    if M2 != M:
+        raise ValueError(f"token dims differ: go_t has {M}, ia_t has {M2}")
+    for name, t in (("go_t", go_t), ("ia_t", ia_t)):
+        if t.dtype != torch.float8_e4m3fn:
+            raise TypeError(f"{name} dtype {t.dtype} is not float8_e4m3fn")
+    if M % 32:
+        raise ValueError(f"M={M} must be a multiple of the MX block size 32")
+    if tuple(go_scale.shape) != (N, M // 32):
+        raise ValueError(f"go_scale shape {tuple(go_scale.shape)} != {(N, M // 32)}")
+    if tuple(ia_scale.shape) != (K, M // 32):
+        raise ValueError(f"ia_scale shape {tuple(ia_scale.shape)} != {(K, M // 32)}")
+    E = group_end_offsets.shape[0]
+    dev = go_t.device
+    g = _u8(_rowmajor(go_t))
+    a = _u8(_rowmajor(ia_t))
+    gs = _u8(_rowmajor(go_scale))
+    as_ = _u8(_rowmajor(ia_scale))
+    offs = _offsets(group_end_offsets, dev)
+    code = _out_code(out_dtype, allowed=(torch.bfloat16, torch.float32))
+    out = torch.empty((E, N, K), dtype=out_dtype, device=dev)
+    lib = _lib.load()
+    ws_bytes = lib.mxgg_wgrad_workspace_size(E, M, N, K)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.mxgg_wgrad(
+        g.data_ptr(), g.stride(0), gs.data_ptr(), gs.stride(0),
+        a.data_ptr(), a.stride(0), as_.data_ptr(), as_.stride(0),
+        offs.data_ptr(), E, M, N, K,
+        out.data_ptr(), code, ws.data_ptr() if ws is not None else None, ws_bytes,
+        _stream_handle(dev))
+    _lib.check(rc)
+    return out

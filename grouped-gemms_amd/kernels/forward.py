@@ -1,0 +1,112 @@
+"""Forward / dgrad MX grouped GEMM on gfx950: ``triton_mxfp8_grouped_mm``.
+
+Drop-in for kernels/forward.py:461-606 of the reference: same name,
+positional order, defaults and return value.  ``output[s:e] = A[s:e] @ B[g]^T``
+per expert group, MX scales per 32 elements of K, fp32 accumulation, one
+rounding to ``out_dtype``.  The work runs in the hand-written HIP kernel of
+libmxgg (``mxgg_grouped_mm``), which builds the expert->tile routing inside
+the kernel from ``group_end_offsets`` (no host sync, no extra launch).
+
+Beyond the reference, the weight may be MXFP4: ``weight`` of dtype
+``torch.float4_e2m1fn_x2`` (or uint8) with last dim K/2, two e2m1 values per
+byte (element 2i in the low nibble), scales per 32 elements of K.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import _offsets, _out_code, _require, _rowmajor, _stream_handle, _u8
+
+# Tile shapes built into libmxgg (BLOCK_M x BLOCK_N); BLOCK_K is fixed at 128.
+BUILT_TILES = ((256, 256), (128, 128))
+
+_FP4_DTYPES = tuple(d for d in (getattr(torch, "float4_e2m1fn_x2", None), torch.uint8) if d is not None)
+
+
+def triton_mxfp8_grouped_mm(
+    input_act: torch.Tensor,
+    weight: torch.Tensor,
+    input_act_scales: torch.Tensor,
+    weight_scales: torch.Tensor,
+    group_end_offsets: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    BLOCK_M: int = None,
+    BLOCK_N: int = None,
+    BLOCK_K: int = None,
+    GROUP_M: int = None,
+    XCD_SWIZZLE: int = None,
+    num_warps: int = None,
+    num_stages: int = None,
+    matrix_instr_nonkdim: int = None,
+    waves_per_eu: int = None,
+    kpack: int = 1,
+    w_cache_modifier: str = None,
+    x_evict_policy: str = None,
+) -> torch.Tensor:
+    """MX grouped GEMM: ``output[g] = input_act[group_g] @ weight[g]^T``.
+
+    Args (kernels/forward.py:485-497):
+        input_act: ``(M, K)`` float8_e4m3fn.
+        weight: ``(E, N, K)`` float8_e4m3fn, or ``(E, N, K/2)`` packed e2m1.
+        input_act_scales: ``(M, K//32)`` e8m0 (uint8 or float8_e8m0fnu).
+        weight_scales: ``(E, N, K//32)`` e8m0.
+        group_end_offsets: ``(E,)`` int32 cumulative group ends.
+        BLOCK_M / BLOCK_N / GROUP_M / XCD_SWIZZLE: tile-shape and schedule
+            requests, honoured when the tile is built (``BUILT_TILES``), else
+            the library picks; ``BLOCK_K`` and the Triton
+            tunables (num_warps, num_stages, matrix_instr_nonkdim,
+            waves_per_eu, kpack, w_cache_modifier, x_evict_policy) are
+            accepted for signature compatibility and have no effect.
+
+    Returns ``(M, N)`` of ``out_dtype``; rows at or past ``offs[-1]`` are left
+    uninitialised, as in the reference.
+    """
+    _require(input_act, "input_act")
+    M, K = input_act.shape
+    E, N, K2 = weight.shape
+    if weight.dtype == torch.float8_e4m3fn:
+        b_fmt = _lib.FMT_E4M3
+        assert K == K2, f"K mismatch: A={K}, B={K2}"
+    elif weight.dtype in _FP4_DTYPES:
+        b_fmt = _lib.FMT_E2M1
+        assert K == 2 * K2, f"K mismatch: A={K}, packed fp4 B={K2} (K/2 expected)"
+    else:
+        raise TypeError(f"weight dtype {weight.dtype} is neither float8_e4m3fn nor packed fp4")
+    if input_act.dtype != torch.float8_e4m3fn:
+        raise TypeError(f"input_act dtype {input_act.dtype} is not float8_e4m3fn")
+    if K % 32:
+        raise ValueError(f"K={K} must be a multiple of the MX block size 32")
+    if tuple(input_act_scales.shape) != (M, K // 32):
+        raise ValueError(f"input_act_scales shape {tuple(input_act_scales.shape)} != {(M, K // 32)}")
+    if tuple(weight_scales.shape) != (E, N, K // 32):
+        raise ValueError(f"weight_scales shape {tuple(weight_scales.shape)} != {(E, N, K // 32)}")
+    if group_end_offsets.numel() != E:
+        raise ValueError(f"group_end_offsets has {group_end_offsets.numel()} entries, weight has E={E}")
+    # Tile requests are hints: a built tile is used, anything else (e.g. a
+    # Triton config copied from the reference's table) falls back to the
+    # library's own choice instead of failing.
+    bm = BLOCK_M or BLOCK_N or 0
+    bn = BLOCK_N or BLOCK_M or 0
+    if (bm, bn) not in BUILT_TILES:
+        bm = bn = 0
+    dev = input_act.device
+    a = _u8(_rowmajor(input_act))
+    b = _u8(_rowmajor(weight))
+    a_s = _u8(_rowmajor(input_act_scales))
+    b_s = _u8(_rowmajor(weight_scales))
+    offs = _offsets(group_end_offsets, dev)
+    out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    code = _out_code(out_dtype)
+    lib = _lib.load()
+    rc = lib.mxgg_grouped_mm(
+        a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),
+        b.data_ptr(), b_fmt, b.stride(1), b.stride(0),
+        b_s.data_ptr(), b_s.stride(1), b_s.stride(0),
+        offs.data_ptr(), E, M, N, K,
+        out.data_ptr(), code, out.stride(0),
+        int(bm), int(bn), int(GROUP_M or 0), int(XCD_SWIZZLE or 0),
+        _stream_handle(dev))
+    _lib.check(rc)
+    return out

@@ -1,0 +1,89 @@
+"""On-GPU MX quantizer (FLOOR e8m0 scale per 32 elements, e4m3 or packed e2m1).
+
+``to_mx`` is the drop-in for the reference's ``to_mx`` (utils.py:67-105):
+same arguments, same ``(scales_uint8, data)`` return order, bit-identical
+bytes and scales, computed by one fused HIP kernel (``mxgg_quantize_mx``)
+instead of ~10 eager torch kernels.  ``to_mx_dim0`` produces
+``to_mx(x.t().contiguous())`` in one pass (``mxgg_quantize_mx_dim0``), the
+"dim1-quantized" layout the weight gradient takes (kernels/backward.py:232).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._common import _require, _stream_handle
+
+_SRC_CODES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16,
+              torch.float32: _lib.DTYPE_F32}
+_FP4 = getattr(torch, "float4_e2m1fn_x2", None)
+
+
+def _src_code(t: torch.Tensor) -> int:
+    if t.dtype not in _SRC_CODES:
+        raise TypeError(f"to_mx input dtype {t.dtype} not one of bf16/fp16/fp32")
+    return _SRC_CODES[t.dtype]
+
+
+def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32):
+    """Quantize ``data`` along its last dim; returns ``(scales_u8, data_q)``.
+
+    ``elem_dtype`` float8_e4m3fn gives ``data_q`` of ``data``'s shape;
+    ``torch.float4_e2m1fn_x2`` gives packed fp4 with the last dim halved
+    (element 2i in the low nibble).  ``scales_u8`` has the last dim divided
+    by 32.  Asserts like the reference (utils.py:78-81).
+    """
+    fp4 = _FP4 is not None and elem_dtype is _FP4
+    assert elem_dtype is torch.float8_e4m3fn or fp4, "only e4m3fn and e2m1fn_x2 supported"
+    assert block_size == 32, "block_size must be 32 (OCP MX)"
+    assert data.shape[-1] % block_size == 0, (
+        f"last dim {data.shape[-1]} must be divisible by block_size {block_size}"
+    )
+    _require(data, "data")
+    code = _src_code(data)
+    shape = tuple(data.shape)
+    L = shape[-1]
+    x = data.reshape(-1, L) if data.dim() != 2 else data
+    if x.stride(-1) != 1 or (x.shape[0] > 1 and (x.stride(0) * x.element_size()) % 16) or x.data_ptr() % 16:
+        x = x.contiguous()
+    rows = x.shape[0]
+    qcols = L // 2 if fp4 else L
+    q = torch.empty((rows, qcols), dtype=torch.uint8, device=data.device)
+    s = torch.empty((rows, L // 32), dtype=torch.uint8, device=data.device)
+    lib = _lib.load()
+    rc = lib.mxgg_quantize_mx(x.data_ptr(), code, rows, L, x.stride(0) if rows > 1 else L,
+                              _lib.FMT_E2M1 if fp4 else _lib.FMT_E4M3,
+                              q.data_ptr(), qcols, s.data_ptr(), L // 32,
+                              _stream_handle(data.device))
+    _lib.check(rc)
+    q = q.view(_FP4 if fp4 else torch.float8_e4m3fn).reshape(shape[:-1] + (qcols,))
+    return s.reshape(shape[:-1] + (L // 32,)), q
+
+
+def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32):
+    """``to_mx(data.t().contiguous())`` for a 2-D ``(R, C)`` tensor in one pass.
+
+    Returns ``(scales (C, R//32) uint8, data (C, R) float8_e4m3fn)``.
+    """
+    assert elem_dtype is torch.float8_e4m3fn, "to_mx_dim0 supports e4m3fn only"
+    assert block_size == 32, "block_size must be 32 (OCP MX)"
+    assert data.dim() == 2, "to_mx_dim0 expects a 2-D tensor"
+    R, C = data.shape
+    assert R % block_size == 0, f"dim 0 ({R}) must be divisible by block_size {block_size}"
+    _require(data, "data")
+    code = _src_code(data)
+    x = data
+    if x.stride(-1) != 1 or (x.stride(0) * x.element_size()) % 16 or x.data_ptr() % 16 \
+            or (C * x.element_size()) % 16:
+        x = x.contiguous()
+    if (C * x.element_size()) % 16:
+        raise ValueError(f"to_mx_dim0 needs dim 1 ({C}) to span a multiple of 16 bytes")
+    q = torch.empty((C, R), dtype=torch.uint8, device=data.device)
+    s = torch.empty((C, R // 32), dtype=torch.uint8, device=data.device)
+    lib = _lib.load()
+    rc = lib.mxgg_quantize_mx_dim0(x.data_ptr(), code, R, C, x.stride(0), _lib.FMT_E4M3,
+                                   q.data_ptr(), R, s.data_ptr(), R // 32,
+                                   _stream_handle(data.device))
+    _lib.check(rc)
+    return s, q.view(torch.float8_e4m3fn)

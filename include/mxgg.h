@@ -1,0 +1,159 @@
+/*
+ * mxgg.h -- C ABI of the MI355X (gfx950) MX-scaled grouped-GEMM library
+ * (libmxgg.so).
+ *
+ * Plain pointers, sizes and strides only.  Every pointer argument named *_ptr
+ * or out* is a device pointer; `stream` is a hipStream_t passed as void*
+ * (NULL = the default stream).  No entry point allocates device memory, frees
+ * it or synchronises the stream: callers own every buffer, and all work is
+ * enqueued on `stream` in order.
+ *
+ * Return value: 0 on success, a negative MXGG_ERR_* for an argument that was
+ * rejected before anything was launched, a positive hipError_t when the HIP
+ * runtime refused a launch.  mxgg_last_error_string() describes the most recent
+ * failure on the calling thread.
+ *
+ * Data formats (the reference's `to_mx` layout, utils.py:67-105):
+ *   e4m3   one byte per element (float8_e4m3fn)
+ *   e2m1   two elements per byte, element 2i in the low nibble
+ *   scales one e8m0 byte per 32 consecutive elements of the quantized
+ *          (contiguous) dimension, value 2**(s-127), plain row-major layout
+ *          (rows, cols/32) with a row stride.
+ * Strides are in ELEMENTS of the pointed-to tensor (bytes for e4m3 and scale
+ * tensors, bytes -- i.e. element pairs -- for packed e2m1 tensors).
+ */
+#ifndef MXGG_H_
+#define MXGG_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXGG_VERSION 1000 /* major*1000 + minor */
+
+/* status codes */
+#define MXGG_OK 0
+#define MXGG_ERR_INVALID_ARG (-1)   /* bad shape, stride, alignment or enum */
+#define MXGG_ERR_UNSUPPORTED (-2)   /* valid request this build does not implement */
+#define MXGG_ERR_WORKSPACE (-3)     /* workspace missing or too small */
+#define MXGG_ERR_NO_DEVICE (-4)     /* no gfx950 device current */
+
+/* element formats (codes match the f8f6f4 MFMA cbsz/blgp encoding) */
+#define MXGG_FMT_E4M3 0
+#define MXGG_FMT_E2M1 4
+
+/* host element types for quantizer inputs and GEMM outputs */
+#define MXGG_DTYPE_BF16 0
+#define MXGG_DTYPE_F16 1
+#define MXGG_DTYPE_F32 2
+
+/* Library version (MXGG_VERSION of the build). */
+int mxgg_version(void);
+
+/* Message for the last failure on this thread ("" if none). */
+const char* mxgg_last_error_string(void);
+
+/* 1 if the current HIP device is a gfx950 part the kernels were built for,
+ * 0 otherwise.  Replaces `_rocm_mxfp8_available` (kernels/_common.py:27) and
+ * `is_MI350` (utils.py:108-115). */
+int mxgg_device_supported(void);
+
+/*
+ * MX quantization along the contiguous last dimension (FLOOR scale mode).
+ * Replaces `to_mx(data, elem_dtype, block_size=32)` (utils.py:67-105).
+ *   src        (rows, cols) of src_dtype, row stride ld_src elements
+ *   elem_fmt   MXGG_FMT_E4M3 (q is (rows, cols) bytes, row stride ld_q) or
+ *              MXGG_FMT_E2M1 (q is (rows, cols/2) packed bytes, row stride ld_q)
+ *   scales     (rows, cols/32) bytes, row stride ld_s
+ * cols must be a multiple of 32.
+ */
+int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
+                     int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
+                     uint8_t* scales, int64_t ld_s, void* stream);
+
+/*
+ * MX quantization along dimension 0 with a transposed output: the result is
+ * exactly to_mx(src.t().contiguous()) -- the "dim1-quantized" operands the
+ * weight gradient takes (kernels/backward.py:232-243).
+ *   src     (rows, cols) of src_dtype, row stride ld_src; rows % 32 == 0
+ *   q       (cols, rows) e4m3 bytes, row stride ld_q (elem_fmt must be E4M3)
+ *   scales  (cols, rows/32) bytes, row stride ld_s
+ */
+int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t cols,
+                          int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
+                          uint8_t* scales, int64_t ld_s, void* stream);
+
+/*
+ * Routing table of the grouped GEMM, in the reference's buffer format
+ * [hist E | start E | total 1 | map grid_m_ub] (int32), where
+ * grid_m_ub = cdiv(M, block_m) + max(E-1, 0) and map[p] = (block << 16) | e or -1.
+ * Replaces `_build_expt_data` / `_expt_data_kernel` (kernels/forward.py:296-365).
+ * The GEMM entry points compute the same table inside the kernel; this entry
+ * point exposes that device code.  out must hold mxgg_routing_words() int32s.
+ */
+int64_t mxgg_routing_words(int E, int64_t M, int block_m);
+int mxgg_build_routing(const int32_t* offs, int E, int64_t M, int block_m, int32_t* out,
+                       void* stream);
+
+/*
+ * Tile schedule of the grouped GEMM: for every program id of the launch grid
+ * (grid_m_ub * cdiv(N, block_n) programs) writes (pid_m, pid_n) or (-1, -1)
+ * for programs that exit, after the XCD swizzle and GROUP_M ordering.
+ * Replaces `_xcd_swizzle` / `_pid_grid` and their use in the GEMM
+ * (kernels/forward.py:31-51, 111-127).  out holds 2 * programs int32s.
+ */
+int64_t mxgg_schedule_programs(int E, int64_t M, int64_t N, int block_m, int block_n);
+int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t N, int block_m,
+                       int block_n, int group_m, int xcd_swizzle, int32_t* out, void* stream);
+
+/*
+ * Forward / dgrad grouped GEMM: out[s:e, :] = A[s:e, :] @ B[g]^T for each group
+ * g with rows [offs[g-1], offs[g]) (offs[-1] = 0), MX scales applied per 32
+ * elements of K, fp32 accumulation, one rounding to out_dtype.
+ * Replaces `triton_mxfp8_grouped_mm` (kernels/forward.py:461-606).
+ *   A        (M, K) e4m3, row stride lda
+ *   A_s      (M, K/32) scales, row stride ldas
+ *   B        (E, N, K) in b_fmt: e4m3 (row stride ldb_n >= K) or e2m1 packed
+ *            (row stride ldb_n >= K/2), expert stride ldb_e
+ *   B_s      (E, N, K/32) scales, row stride ldbs_n, expert stride ldbs_e
+ *   offs     (E,) int32 cumulative group ends, device memory, nondecreasing,
+ *            offs[E-1] <= M
+ *   out      (M, N) of out_dtype, row stride ldo.  Rows >= offs[E-1] are not
+ *            written (as in the reference).
+ *   block_m, block_n, group_m, xcd_swizzle: 0 = library choice; otherwise a
+ *            request honoured when the build has that tile shape.
+ * K must be a multiple of 32 (of 128 for the e2m1 weight format).
+ */
+int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
+                    const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
+                    const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
+                    const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                    void* out, int out_dtype, int64_t ldo,
+                    int block_m, int block_n, int group_m, int xcd_swizzle, void* stream);
+
+/*
+ * Weight-gradient grouped GEMM: out[g] = GO[:, s:e] @ IA[:, s:e]^T, shape (E, N, K),
+ * a reduction over each group's token range; an empty group gives zeros.
+ * Replaces `triton_mxfp8_wgrad` (kernels/backward.py:217-305), including its
+ * store of bf16-rounded values whatever out_dtype is (backward.py:103, 214).
+ *   go_t  (N, M) e4m3, row stride ld_go;   go_s (N, M/32), row stride ld_gos
+ *   ia_t  (K, M) e4m3, row stride ld_ia;   ia_s (K, M/32), row stride ld_ias
+ *   offs  (E,) int32 cumulative group ends, multiples of 32, offs[E-1] <= M
+ *   out   (E, N, K) of out_dtype (BF16 or F32), contiguous
+ *   workspace / ws_bytes: device scratch of at least
+ *         mxgg_wgrad_workspace_size(E, M, N, K) bytes (may be NULL when that is 0)
+ */
+size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
+int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
+               const uint8_t* ia_t, int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias,
+               const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+               void* out, int out_dtype, void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXGG_H_ */

@@ -1,0 +1,302 @@
+"""GPU parity for the grouped GEMMs against the oracle's dequantize -> fp64
+per-group matmul (kernels/forward.py:81-294, kernels/backward.py:31-215).
+
+Tolerances: relative Frobenius error <= 1e-2 vs the
+dequantize-then-matmul reference, and SQNR >= 27 dB vs the unquantized bf16
+product.  The kernel's only rounding is fp32 accumulation plus one bf16
+store, so the observed error is ~1e-3; the tests also check that bound at
+3e-3 so a real regression (a dropped block, a wrong scale) cannot hide
+under the loose gate.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits_u8, bits_u16, f32, randn_bf16, seeded_offs
+from oracle import mx_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_FRO_GATE = 1e-2
+REL_FRO_TIGHT = 3e-3
+SQNR_GATE = 27.0
+
+
+def _quant(x_bf16_cpu, gpu):
+    import kernels
+    s, q = kernels.to_mx(x_bf16_cpu.to(gpu))
+    return s, q
+
+
+def _fwd_case(E, M, N, K, offs, gpu, seed=0, std_b=0.02, out_dtype=torch.bfloat16, **kw):
+    import kernels
+    a = randn_bf16((M, K), 1.0, seed)
+    b = randn_bf16((E, N, K), std_b, seed + 1)
+    sa, qa = _quant(a, gpu)
+    sb, qb = _quant(b, gpu)
+    offs_t = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    out = kernels.triton_mxfp8_grouped_mm(qa, qb, sa, sb, offs_t, out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    ref = O.grouped_mm(bits_u8(qa), bits_u8(sa), bits_u8(qb), bits_u8(sb), offs)
+    hp = O.grouped_mm_hp(O.bf16_bits_to_f32(bits_u16(a)), O.bf16_bits_to_f32(bits_u16(b)), offs)
+    return f32(out), ref, hp
+
+
+def _assert_close(out, ref, hp=None, rows=None, tight=True):
+    if rows is not None:
+        out, ref = out[:rows], ref[:rows]
+        hp = hp[:rows] if hp is not None else None
+    assert np.isfinite(out).all()
+    err = O.rel_fro(ref, out)
+    assert err <= REL_FRO_GATE, err
+    if tight:
+        assert err <= REL_FRO_TIGHT, err
+    if hp is not None:
+        assert O.sqnr_db(hp, out) >= SQNR_GATE
+
+
+@pytest.mark.parametrize("E,M,N,K,std_b", [(4, 1024, 512, 512, 0.02),      # BASELINE cfg1
+                                           (1, 1024, 1024, 1024, 1.0),    # test_correctness.py:70-73
+                                           (8, 1024, 4096, 2048, 1.0),
+                                           (4, 1024, 2048, 2048, 1.0),
+                                           (8, 2048, 5120, 2048, 1.0)])
+def test_fwd_reference_shapes(gpu, E, M, N, K, std_b):
+    """cfg1 plus the four shapes of the reference's correctness script."""
+    offs = seeded_offs(E, M, seed=E * 1000 + N)
+    out, ref, hp = _fwd_case(E, M, N, K, offs, gpu, seed=E + K, std_b=std_b)
+    _assert_close(out, ref, hp)
+
+
+def test_fwd_golden_cfg1(gpu):
+    """Committed cfg1 fixture: GPU output vs the frozen oracle output."""
+    import os
+    import kernels
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1.npz"))
+    dev = gpu
+    qa = torch.from_numpy(z["a_q"]).to(dev).view(torch.float8_e4m3fn)
+    qb = torch.from_numpy(z["b_q"]).to(dev).view(torch.float8_e4m3fn)
+    sa = torch.from_numpy(z["a_scales"]).to(dev)
+    sb = torch.from_numpy(z["b_scales"]).to(dev)
+    offs = torch.from_numpy(z["offs"]).to(dev)
+    out = kernels.triton_mxfp8_grouped_mm(qa, qb, sa, sb, offs)
+    torch.cuda.synchronize()
+    ref = O.bf16_bits_to_f32(z["out_bf16"])
+    got = f32(out)
+    assert O.rel_fro(ref, got) <= REL_FRO_TIGHT
+    # bf16 outputs: at most a 1-ulp difference from the frozen bf16 result
+    d = np.abs(bits_u16(out).astype(np.int32) - z["out_bf16"].astype(np.int32))
+    assert (d <= 1).mean() > 0.99
+
+
+@pytest.mark.parametrize("tile", [(128, 128), (256, 256)])
+@pytest.mark.parametrize("offs", [[0, 32, 32, 300 - 300 % 32, 640],   # empty groups, ragged
+                                  [640, 640, 640],                      # all rows in group 0
+                                  [7, 100, 333, 640]])                  # not multiples of 32
+def test_fwd_ragged_and_empty_groups(gpu, tile, offs):
+    E, M, N, K = len(offs), 640, 384, 256
+    out, ref, hp = _fwd_case(E, M, N, K, offs, gpu, seed=3, std_b=1.0,
+                             BLOCK_M=tile[0], BLOCK_N=tile[1])
+    _assert_close(out, ref, hp, rows=offs[-1])
+
+
+def test_fwd_rows_past_last_offset_untouched(gpu):
+    import kernels
+    E, M, N, K = 2, 512, 256, 128
+    offs = [96, 320]
+    a = randn_bf16((M, K), 1.0, 1)
+    b = randn_bf16((E, N, K), 1.0, 2)
+    sa, qa = _quant(a, gpu)
+    sb, qb = _quant(b, gpu)
+    out = kernels.triton_mxfp8_grouped_mm(qa, qb, sa, sb, torch.tensor(offs, dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    ref = O.grouped_mm(bits_u8(qa), bits_u8(sa), bits_u8(qb), bits_u8(sb), offs)
+    _assert_close(f32(out), ref, rows=320)
+
+
+@pytest.mark.parametrize("N,K", [(200, 96), (33, 160), (4096, 32)])
+def test_fwd_odd_shapes(gpu, N, K):
+    """N not a multiple of the tile / of 4, K not a multiple of 128 (masked tail)."""
+    E, M = 3, 448
+    offs = [64, 256, 448]
+    out, ref, hp = _fwd_case(E, M, N, K, offs, gpu, seed=N + K, std_b=1.0)
+    _assert_close(out, ref, hp)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_fwd_out_dtypes(gpu, out_dtype):
+    E, M, N, K = 2, 512, 256, 512
+    offs = [192, 512]
+    out, ref, hp = _fwd_case(E, M, N, K, offs, gpu, seed=9, std_b=0.1, out_dtype=out_dtype)
+    err = O.rel_fro(ref, out)
+    # fp32 output: only the MFMA's internal fp32 accumulation differs from fp64
+    assert err <= (1e-4 if out_dtype == torch.float32 else 1e-3), err
+
+
+def test_fwd_group_m_xcd_options(gpu):
+    E, M, N, K = 3, 1536, 1024, 256
+    offs = [512, 1024, 1536]
+    outs = []
+    for gm, x in ((1, 1), (4, 8), (8, 4), (16, 8)):
+        out, ref, _ = _fwd_case(E, M, N, K, offs, gpu, seed=4, GROUP_M=gm, XCD_SWIZZLE=x)
+        _assert_close(out, ref)
+        outs.append(out)
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])     # schedule never changes the numbers
+
+
+def test_dgrad_shape(gpu):
+    """dgrad = same op with grad_out (M, N) against W^T (E, K, N) quantized along N."""
+    import kernels
+    E, M, N, K = 4, 1024, 512, 768
+    offs = seeded_offs(E, M, seed=21)
+    go = randn_bf16((M, N), 1.0, 30)
+    w = randn_bf16((E, N, K), 0.02, 31)
+    wt = w.transpose(-2, -1).contiguous()            # (E, K, N)
+    sg, qg = _quant(go, gpu)
+    sw, qw = _quant(wt, gpu)
+    out = kernels.triton_mxfp8_grouped_mm(qg, qw, sg, sw, torch.tensor(offs, device=gpu))
+    torch.cuda.synchronize()
+    ref = O.grouped_mm(bits_u8(qg), bits_u8(sg), bits_u8(qw), bits_u8(sw), offs)
+    hp = O.grouped_mm_hp(f32(go), f32(wt), offs)
+    _assert_close(f32(out), ref, hp)
+
+
+def test_fwd_mxfp4_weights(gpu):
+    """Mixed e4m3 activations x e2m1 weights (f8f6f4 MFMA with the fp4 B format)."""
+    import kernels
+    fp4 = torch.float4_e2m1fn_x2
+    E, M, N, K = 4, 1024, 512, 512
+    offs = seeded_offs(E, M, seed=44)
+    a = randn_bf16((M, K), 1.0, 40)
+    b = randn_bf16((E, N, K), 0.02, 41)
+    sa, qa = _quant(a, gpu)
+    sb, qb = kernels.to_mx(b.to(gpu), elem_dtype=fp4)
+    out = kernels.triton_mxfp8_grouped_mm(qa, qb, sa, sb, torch.tensor(offs, device=gpu))
+    torch.cuda.synchronize()
+    ref = O.grouped_mm(bits_u8(qa), bits_u8(sa), bits_u8(qb), bits_u8(sb), offs, b_elem="e2m1")
+    _assert_close(f32(out), ref)
+    # fp4 weights lose more than fp8 vs bf16; only check it is sane
+    hp = O.grouped_mm_hp(f32(a), f32(b), offs)
+    assert O.sqnr_db(hp, f32(out)) > 12.0
+
+
+def test_fwd_full_size_cfg2(gpu):
+    """BASELINE config 2 at full size (E=1, M=16640, N=K=2048) against a GPU
+    fp32 dequantize -> matmul of the same quantized operands."""
+    import kernels
+    M, N, K = 16640, 2048, 2048
+    g = torch.Generator(device=gpu).manual_seed(1)
+    a = torch.randn((M, K), device=gpu, generator=g).to(torch.bfloat16)
+    b = (torch.randn((1, N, K), device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    sa, qa = kernels.to_mx(a)
+    sb, qb = kernels.to_mx(b)
+    out = kernels.triton_mxfp8_grouped_mm(qa, qb, sa, sb, torch.tensor([M], dtype=torch.int32, device=gpu))
+
+    def deq(q, s):
+        v = q.float().reshape(*q.shape[:-1], -1, 32)
+        return (v * torch.exp2(s.float() - 127).unsqueeze(-1)).reshape(q.shape)
+
+    ref = deq(qa, sa) @ deq(qb, sb)[0].t()
+    err = (out.float() - ref).norm() / ref.norm()
+    assert err.item() <= REL_FRO_TIGHT
+    hp = a.float() @ b[0].float().t()
+    sq = 20 * torch.log10(hp.norm() / (hp - out.float()).norm())
+    assert sq.item() >= SQNR_GATE
+
+
+# ---------------------------------------------------------------- wgrad
+
+def _wgrad_case(E, M, N, K, offs, gpu, seed=0, out_dtype=torch.bfloat16):
+    import kernels
+    go = randn_bf16((M, N), 1.0, seed)
+    ia = randn_bf16((M, K), 1.0, seed + 1)
+    sg, qg = kernels.to_mx_dim0(go.to(gpu))        # (N, M), (N, M/32)
+    si, qi = kernels.to_mx_dim0(ia.to(gpu))        # (K, M), (K, M/32)
+    out = kernels.triton_mxfp8_wgrad(qg, sg, qi, si, torch.tensor(offs, dtype=torch.int32, device=gpu),
+                                     out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref = O.wgrad(bits_u8(qg), bits_u8(sg), bits_u8(qi), bits_u8(si), offs)
+    return out, ref, go, ia
+
+
+@pytest.mark.parametrize("E,M,N,K", [(4, 1024, 512, 512), (1, 1024, 256, 384), (8, 2048, 512, 256)])
+def test_wgrad_random(gpu, E, M, N, K):
+    offs = seeded_offs(E, M, seed=M + E)
+    out, ref, go, ia = _wgrad_case(E, M, N, K, offs, gpu, seed=E)
+    _assert_close(f32(out), ref)
+    # vs unquantized bf16 product per group
+    g32, i32 = f32(go), f32(ia)
+    prev = 0
+    hp = np.zeros_like(ref)
+    for e, end in enumerate(offs):
+        hp[e] = g32[prev:end].T.astype(np.float64) @ i32[prev:end].astype(np.float64)
+        prev = end
+    assert O.sqnr_db(hp, f32(out)) >= SQNR_GATE
+
+
+def test_wgrad_empty_and_unaligned_groups(gpu):
+    """Empty groups give zeros; group bounds at 32 but not 128 multiples."""
+    E, M, N, K = 5, 1024, 320, 288
+    offs = [0, 160, 160, 544, 1024]
+    out, ref, _, _ = _wgrad_case(E, M, N, K, offs, gpu, seed=12)
+    o = f32(out)
+    assert (o[0] == 0).all() and (o[2] == 0).all()
+    _assert_close(o, ref)
+
+
+def test_wgrad_fp32_out_is_bf16_rounded(gpu):
+    """The reference stores acc.to(bf16) even for out_dtype=float32 (backward.py:103)."""
+    E, M, N, K = 2, 512, 256, 256
+    offs = [256, 512]
+    out, ref, _, _ = _wgrad_case(E, M, N, K, offs, gpu, seed=13, out_dtype=torch.float32)
+    assert out.dtype == torch.float32
+    o = out.cpu()
+    assert torch.equal(o, o.to(torch.bfloat16).float())
+    _assert_close(f32(out), ref)
+
+
+# ---------------------------------------------------------------- routing / schedule
+
+def test_routing_table_kat(gpu):
+    from kernels import _lib
+    lib = _lib.load()
+    offs = torch.tensor([96, 352, 640, 1024], dtype=torch.int32, device=gpu)
+    n = lib.mxgg_routing_words(4, 1024, 128)
+    out = torch.full((n,), -7, dtype=torch.int32, device=gpu)
+    _lib.check(lib.mxgg_build_routing(offs.data_ptr(), 4, 1024, 128, out.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    want = [96, 256, 288, 384, 0, 96, 352, 640, 9,
+            0x0, 0x1, 0x10001, 0x2, 0x10002, 0x20002, 0x3, 0x10003, 0x20003, -1, -1]
+    assert out.cpu().tolist() == want
+
+
+@pytest.mark.parametrize("E,M,BM", [(1, 16640, 256), (8, 16640, 256), (8, 16640, 128), (70, 4096, 128),
+                                    (200, 8192, 64)])
+def test_routing_matches_oracle(gpu, E, M, BM):
+    from kernels import _lib
+    lib = _lib.load()
+    offs = seeded_offs(E, M, seed=E * 7 + BM)
+    n = lib.mxgg_routing_words(E, M, BM)
+    out = torch.empty((n,), dtype=torch.int32, device=gpu)
+    _lib.check(lib.mxgg_build_routing(torch.tensor(offs, device=gpu).data_ptr(), E, M, BM, out.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref, _ = O.routing_table(offs, M, BM)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("E,M,N,BM,BN,GM,X", [(8, 16640, 8192, 256, 256, 8, 8), (1, 16640, 2048, 128, 128, 16, 4),
+                                              (3, 1000, 640, 128, 128, 4, 8), (5, 4096, 1024, 256, 256, 1, 1)])
+def test_tile_schedule_matches_oracle(gpu, E, M, N, BM, BN, GM, X):
+    from kernels import _lib
+    lib = _lib.load()
+    offs = seeded_offs(E, M - M % 32, seed=N) if M % 32 == 0 else np.array([100, 500, 1000][:E], np.int32)
+    progs = lib.mxgg_schedule_programs(E, M, N, BM, BN)
+    out = torch.empty((2 * progs,), dtype=torch.int32, device=gpu)
+    _lib.check(lib.mxgg_tile_schedule(torch.tensor(offs, device=gpu).data_ptr(), E, M, N, BM, BN, GM, X,
+                                      out.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref = O.tile_schedule(offs, M, N, BM, BN, GM, X)
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1, 2), ref)
