@@ -1,0 +1,249 @@
+"""Benchmark of the MX grouped-GEMM hot path on one MI355X.
+
+Workload (BASELINE.json configs 3 and 4): the reference's 36-shape Llama4
+sweep, E in {1,2,4,8}, M = 16640 tokens, N, K in {2048, 5120, 8192}, run as
+  * forward  out = A (M,K) @ B[g]^T (E,N,K)            (the headline)
+  * dgrad    out = grad_out (M,N) @ W^T[g]^T (E,K,N)
+  * wgrad    out[g] = grad_out[g]^T @ A[g]  -> (E,N,K)
+with jagged offsets drawn exactly like the reference's bench (random.seed(123),
+``generate_jagged_offs`` in config order; bench.py:113-122, 250-257).  Inputs
+are synthetic (A, grad_out ~ N(0,1), weights ~ N(0,0.02)), quantized on the GPU
+before timing; quantization is outside the timed region, as in the reference
+(bench.py:126-130).
+
+Timed region per shape: the full drop-in Python call (output allocation, the
+C-ABI call, the in-kernel routing and the GEMM), bracketed by HIP events on
+the current stream after a 512 MB cache flush; median over ``--steps`` reps
+after ``--warmup`` reps.  TFLOPs = 2*M*N*K / t (bench.py:200).  A "step" is one
+call per shape over all 108 problems; ms_per_step is the sum of the medians.
+
+Prints ONE JSON line on stdout; progress and the per-shape table go to stderr
+and to gpurun_out/bench_detail.json when that directory exists.
+"""
+
+from __future__ import annotations
+
+import argparse
+import itertools
+import json
+import math
+import os
+import platform
+import random
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "grouped-gemms_amd"))
+
+PEAK_MXFP8_TFLOPS = 5000.0          # MI355X published dense MXFP8 / FP8 peak
+REF_FWD_GEOMEAN_TFLOPS = 1498.8     # reference README table, 36-shape fwd geomean (MI355X)
+M_TOKENS = 16640
+SHAPES = [(e, n, k) for e, n, k in itertools.product((1, 2, 4, 8), (2048, 5120, 8192), (2048, 5120, 8192))]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_call(fn, steps: int, warmup: int, flush_buf):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        flush_buf.zero_()
+        st[i].record()
+        fn()
+        en[i].record()
+    torch.cuda.synchronize()
+    ts = [a.elapsed_time(b) for a, b in zip(st, en)]
+    return statistics.median(ts), sum(ts) / len(ts)
+
+
+def geomean(xs):
+    return math.exp(sum(math.log(x) for x in xs) / len(xs))
+
+
+def cpu_baseline(budget_s: float):
+    """Oracle CPU path (dequantize -> per-group fp32 matmul -> bf16) on a bounded
+    sample of the workload: the forward of BASELINE config 2's shape family
+    (E=1, N=K=2048) on a row slice of M sized to about `budget_s` seconds."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import mx_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(1)
+    N = K = 2048
+    rows = 2048
+    a = rng.standard_normal((rows, K), dtype=np.float32)
+    b = (rng.standard_normal((1, N, K), dtype=np.float32) * 0.02).astype(np.float32)
+    sa, qa = O.to_mx(a, src="f32")
+    sb, qb = O.to_mx(b, src="f32")
+    offs = np.array([rows], dtype=np.int32)
+    flops = 2.0 * rows * N * K
+    t_total, reps = 0.0, 0
+    while t_total < budget_s or reps < 2:
+        t0 = time.perf_counter()
+        out = O.grouped_mm(qa, sa, qb, sb, offs, dtype=np.float32)
+        O.f32_to_bf16_bits(out)
+        t_total += time.perf_counter() - t0
+        reps += 1
+    per = t_total / reps
+    return {"value": round(flops / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle fwd (dequantize e4m3+e8m0 -> fp32 matmul -> bf16), E=1, M={rows}, "
+                      f"N=K=2048, {reps} reps in {t_total:.1f}s, numpy/BLAS threads={threads}, "
+                      f"cpu={platform.processor() or platform.machine()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30, help="timed reps per shape")
+    ap.add_argument("--warmup", type=int, default=10, help="untimed reps per shape")
+    ap.add_argument("--only", choices=("all", "fwd", "dgrad", "wgrad"), default="all")
+    ap.add_argument("--shapes", type=int, default=36, help="first N shapes of the sweep")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import kernels
+    from kernels import to_mx, to_mx_dim0, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
+    from utils import generate_jagged_offs
+
+    if not kernels._rocm_mxfp8_available or not torch.cuda.is_available():
+        raise SystemExit("libmxgg / GPU unavailable")
+    dev = torch.device("cuda:0")
+    torch.manual_seed(123)
+    random.seed(123)
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
+    shapes = SHAPES[: args.shapes]
+    offs_by_shape = {s: generate_jagged_offs(s[0], M_TOKENS, multiple_of=32, device=dev) for s in shapes}
+
+    rows = []
+    kernel_ms = {"fwd": 0.0, "dgrad": 0.0}
+    kernel_flops = {"fwd": 0.0, "dgrad": 0.0}
+    kernel_launches = {"fwd": 0, "dgrad": 0}
+    t_start = time.time()
+    for (E, N, K) in shapes:
+        M = M_TOKENS
+        offs = offs_by_shape[(E, N, K)]
+        flops = 2.0 * M * N * K
+        row = {"E": E, "M": M, "N": N, "K": K}
+        if args.only in ("all", "fwd"):
+            a = torch.randn((M, K), device=dev).to(torch.bfloat16)
+            w = (torch.randn((E, N, K), device=dev) * 0.02).to(torch.bfloat16)
+            sa, qa = to_mx(a)
+            sw, qw = to_mx(w)
+            del a, w
+            med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs),
+                                  args.steps, args.warmup, flush)
+            row["fwd_us"] = med * 1e3
+            row["fwd_tflops"] = flops / (med * 1e-3) / 1e12
+            kernel_ms["fwd"] += mean * args.steps
+            kernel_flops["fwd"] += flops * args.steps
+            kernel_launches["fwd"] += args.steps
+            del qa, qw, sa, sw
+        if args.only in ("all", "dgrad"):
+            go = torch.randn((M, N), device=dev).to(torch.bfloat16)
+            wt = (torch.randn((E, K, N), device=dev) * 0.02).to(torch.bfloat16)   # W^T (E,K,N)
+            sg, qg = to_mx(go)
+            st_, qt = to_mx(wt)
+            del go, wt
+            med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qg, qt, sg, st_, offs),
+                                  args.steps, args.warmup, flush)
+            row["dgrad_us"] = med * 1e3
+            row["dgrad_tflops"] = flops / (med * 1e-3) / 1e12
+            kernel_ms["dgrad"] += mean * args.steps
+            kernel_flops["dgrad"] += flops * args.steps
+            kernel_launches["dgrad"] += args.steps
+            del qg, qt, sg, st_
+        if args.only in ("all", "wgrad"):
+            go = torch.randn((M, N), device=dev).to(torch.bfloat16)
+            ia = torch.randn((M, K), device=dev).to(torch.bfloat16)
+            sg, qg = to_mx_dim0(go)          # (N, M)
+            si, qi = to_mx_dim0(ia)          # (K, M)
+            del go, ia
+            med, _ = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs),
+                               args.steps, args.warmup, flush)
+            row["wgrad_us"] = med * 1e3
+            row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
+            del qg, qi, sg, si
+        torch.cuda.empty_cache()
+        rows.append(row)
+        log(json.dumps({k: (round(v, 1) if isinstance(v, float) else v) for k, v in row.items()}))
+
+    def gm(key):
+        vals = [r[key] for r in rows if key in r]
+        return geomean(vals) if vals else None
+
+    fwd_gm, dgrad_gm, wgrad_gm = gm("fwd_tflops"), gm("dgrad_tflops"), gm("wgrad_tflops")
+    ms_per_step = sum(r.get("fwd_us", 0) + r.get("dgrad_us", 0) + r.get("wgrad_us", 0) for r in rows) / 1e3
+    per_e = {}
+    for e in (1, 2, 4, 8):
+        v = [r["fwd_tflops"] for r in rows if r["E"] == e and "fwd_tflops" in r]
+        if v:
+            per_e[str(e)] = round(geomean(v), 1)
+
+    # roofline of the dominant kernel (the grouped GEMM kernel, fwd + dgrad launches)
+    kms = kernel_ms["fwd"] + kernel_ms["dgrad"]
+    kfl = kernel_flops["fwd"] + kernel_flops["dgrad"]
+    nl = kernel_launches["fwd"] + kernel_launches["dgrad"]
+    achieved = kfl / (kms * 1e-3) / 1e12 if kms else None
+    roofline = {"bound": "mfma", "achieved": round(achieved, 1) if achieved else None,
+                "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4) if achieved else None,
+                "traffic": None,
+                "kernel": "mxgg::fwd_kernel (forward + dgrad launches of the sweep)",
+                "avg_launch_us": round(kms / nl * 1e3, 2) if nl else None,
+                "launches": nl}
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
+    value = fwd_gm if fwd_gm is not None else (dgrad_gm or wgrad_gm)
+    line = {
+        "metric": "geomean MXFP8 grouped-GEMM TFLOPs (% of MXFP8 peak), fwd/dgrad/wgrad, 1 GPU",
+        "value": round(value, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(fwd_gm / REF_FWD_GEOMEAN_TFLOPS, 4) if fwd_gm else None,
+        "dtype": "mxfp8-e4m3 (e8m0 per-32 scales, fp32 accumulate, bf16 out)",
+        "data": "synthetic",
+        "config": {"workload": f"{len(rows)}-shape Llama4 MoE sweep, E in (1,2,4,8), M=16640, "
+                               f"N,K in (2048,5120,8192); fwd (headline value), dgrad, wgrad",
+                   "offs": "generate_jagged_offs, multiples of 32, random.seed(123)"},
+        "fwd_geomean_tflops": round(fwd_gm, 1) if fwd_gm else None,
+        "dgrad_geomean_tflops": round(dgrad_gm, 1) if dgrad_gm else None,
+        "wgrad_geomean_tflops": round(wgrad_gm, 1) if wgrad_gm else None,
+        "fwd_pct_of_peak": round(100 * fwd_gm / PEAK_MXFP8_TFLOPS, 2) if fwd_gm else None,
+        "fwd_geomean_by_E": per_e,
+        "baseline_note": "vs_baseline = fwd geomean / 1498.8 TFLOP/s (reference README table, MI355X)",
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "wall_s": round(time.time() - t_start, 1),
+    }
+    outdir = os.path.join(ROOT, "gpurun_out")
+    if os.path.isdir(outdir):
+        with open(os.path.join(outdir, "bench_detail.json"), "w") as f:
+            json.dump({"summary": line, "rows": rows}, f, indent=1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

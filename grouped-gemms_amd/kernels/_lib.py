@@ -61,25 +61,28 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib = None
-_load_error: str | None = None
+
+
+def _open(path: str) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise NotImplementedError(f"{path} not built (run make -C grouped-gemms_amd/csrc)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:
-    """Load (once) and return the library with typed entry points."""
-    global _lib, _load_error
+    """Return the library with typed entry points (loaded once for LIB_PATH)."""
+    global _lib
+    if path != LIB_PATH:
+        return _open(path)
     with _lock:
-        if _lib is not None:
-            return _lib
-        if not os.path.exists(path):
-            _load_error = f"{path} not built (run make -C grouped-gemms_amd/csrc)"
-            raise NotImplementedError(_load_error)
-        lib = ctypes.CDLL(path)
-        for name, (res, args) in SIGNATURES.items():
-            fn = getattr(lib, name)
-            fn.restype = res
-            fn.argtypes = args
-        _lib = lib
-        return lib
+        if _lib is None:
+            _lib = _open(path)
+        return _lib
 
 
 def available() -> bool:

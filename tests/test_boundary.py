@@ -1,0 +1,164 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads and exports every
+symbol include/mxgg.h declares, rejects bad arguments before touching the GPU,
+and the Python surface keeps the reference's names, signatures and errors
+(kernels/__init__.py:17-25, kernels/forward.py:461-484, kernels/backward.py:217-229,
+utils.py:28-115)."""
+
+import ctypes
+import inspect
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mxgg.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mxgg_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from kernels import _lib
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    names = _declared_functions()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_version_and_error_string():
+    from kernels import _lib
+    lib = _lib.load()
+    assert lib.mxgg_version() == 1000
+    assert isinstance(lib.mxgg_last_error_string(), bytes)
+
+
+def test_pure_size_helpers():
+    from kernels import _lib
+    lib = _lib.load()
+    assert lib.mxgg_routing_words(4, 1024, 128) == 2 * 4 + 1 + 8 + 3
+    assert lib.mxgg_routing_words(1, 16640, 256) == 2 + 1 + 65
+    assert lib.mxgg_schedule_programs(8, 16640, 8192, 256, 256) == (65 + 7) * 32
+    assert lib.mxgg_routing_words(0, 10, 128) == 0
+
+
+@pytest.mark.parametrize("args,needle", [
+    (dict(b_fmt=3), "weight format"),
+    (dict(out_dtype=9), "out_dtype"),
+    (dict(E=0), "E=0"),
+    (dict(K=48), "multiple of 32"),
+    (dict(lda=16), "row stride"),
+    (dict(lda=72, K=64), "16-byte aligned"),
+])
+def test_grouped_mm_validation_without_gpu(args, needle):
+    """Invalid requests are rejected (MXGG_ERR_INVALID_ARG) before any HIP call."""
+    from kernels import _lib
+    lib = _lib.load()
+    p = dict(A=16, lda=64, As=16, ldas=2, B=16, b_fmt=0, ldb_n=64, ldb_e=64 * 64, Bs=16, ldbs_n=2,
+             ldbs_e=128, offs=16, E=1, M=64, N=64, K=64, out=16, out_dtype=0, ldo=64)
+    p.update(args)
+    rc = lib.mxgg_grouped_mm(p["A"], p["lda"], p["As"], p["ldas"], p["B"], p["b_fmt"], p["ldb_n"],
+                             p["ldb_e"], p["Bs"], p["ldbs_n"], p["ldbs_e"], p["offs"], p["E"], p["M"],
+                             p["N"], p["K"], p["out"], p["out_dtype"], p["ldo"], 0, 0, 0, 0, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    assert needle in lib.mxgg_last_error_string().decode()
+
+
+def test_wgrad_and_quant_validation_without_gpu():
+    from kernels import _lib
+    lib = _lib.load()
+    rc = lib.mxgg_wgrad(16, 48, 16, 1, 16, 48, 16, 1, 16, 1, 48, 8, 8, 16, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 32" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_quantize_mx(16, 0, 4, 40, 40, 0, 16, 40, 16, 2, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"divisible by block_size 32" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_quantize_mx(16, 5, 4, 64, 64, 0, 16, 64, 16, 2, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    rc = lib.mxgg_quantize_mx_dim0(16, 0, 40, 64, 64, 0, 16, 40, 16, 1, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    rc = lib.mxgg_quantize_mx_dim0(16, 0, 64, 64, 64, 4, 16, 64, 16, 2, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    # empty problems are valid no-ops that never reach the device
+    assert lib.mxgg_quantize_mx(None, 0, 0, 64, 64, 0, None, 64, None, 2, None) == 0
+
+
+def test_import_surface_matches_reference():
+    import kernels
+    for name in ("triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "_rocm_mxfp8_available"):
+        assert hasattr(kernels, name)
+    assert isinstance(kernels._rocm_mxfp8_available, bool)
+    import utils
+    for name in ("to_mx", "generate_jagged_offs", "benchmark_cuda_function_in_microseconds", "is_MI350"):
+        assert callable(getattr(utils, name))
+
+
+def test_forward_signature_matches_reference():
+    from kernels import triton_mxfp8_grouped_mm
+    sig = inspect.signature(triton_mxfp8_grouped_mm)
+    want = ["input_act", "weight", "input_act_scales", "weight_scales", "group_end_offsets", "out_dtype",
+            "BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "XCD_SWIZZLE", "num_warps", "num_stages",
+            "matrix_instr_nonkdim", "waves_per_eu", "kpack", "w_cache_modifier", "x_evict_policy"]
+    assert list(sig.parameters) == want
+    assert sig.parameters["out_dtype"].default is torch.bfloat16
+    assert sig.parameters["kpack"].default == 1
+    assert all(sig.parameters[n].default is None for n in want[6:15] if n != "kpack")
+
+
+def test_wgrad_signature_matches_reference():
+    from kernels import triton_mxfp8_wgrad
+    sig = inspect.signature(triton_mxfp8_wgrad)
+    assert list(sig.parameters) == ["go_t", "go_scale", "ia_t", "ia_scale", "group_end_offsets", "out_dtype",
+                                    "BLOCK_N", "BLOCK_K", "BLOCK_M", "num_warps", "num_stages"]
+    d = {k: v.default for k, v in sig.parameters.items()}
+    assert (d["BLOCK_N"], d["BLOCK_K"], d["BLOCK_M"], d["num_warps"], d["num_stages"]) == (256, 256, 64, 8, 2)
+
+
+def test_to_mx_signature_matches_reference():
+    import utils
+    sig = inspect.signature(utils.to_mx)
+    assert list(sig.parameters) == ["data", "elem_dtype", "block_size"]
+    assert sig.parameters["block_size"].default == 32
+
+
+def test_cpu_tensors_fail_loudly():
+    """No CPU fallback: the operators refuse host tensors."""
+    from kernels import to_mx, triton_mxfp8_grouped_mm
+    a = torch.zeros((64, 64), dtype=torch.float8_e4m3fn)
+    b = torch.zeros((1, 64, 64), dtype=torch.float8_e4m3fn)
+    sa = torch.zeros((64, 2), dtype=torch.uint8)
+    sb = torch.zeros((1, 64, 2), dtype=torch.uint8)
+    with pytest.raises(TypeError):
+        triton_mxfp8_grouped_mm(a, b, sa, sb, torch.tensor([64], dtype=torch.int32))
+    with pytest.raises(TypeError):
+        to_mx(torch.zeros((4, 64), dtype=torch.bfloat16))
+
+
+def test_shape_errors_match_reference_types():
+    from kernels import triton_mxfp8_grouped_mm
+    a = torch.zeros((64, 64), dtype=torch.float8_e4m3fn, device="meta")
+    b = torch.zeros((1, 64, 96), dtype=torch.float8_e4m3fn, device="meta")
+    with pytest.raises((AssertionError, TypeError)):
+        triton_mxfp8_grouped_mm(a, b, None, None, None)
+
+
+def test_missing_library_raises_not_implemented(tmp_path):
+    from kernels import _lib
+    with pytest.raises(NotImplementedError):
+        _lib.load(str(tmp_path / "missing_libmxgg.so"))
+
+
+def test_generate_jagged_offs_same_draws_as_reference_algorithm():
+    import random
+    import utils
+    random.seed(123)
+    o = utils.generate_jagged_offs(8, 16640, device="cpu")
+    random.seed(123)
+    want = sorted(random.sample(list(range(32, 16641, 32))[:-1], 7)) + [16640]
+    assert o.tolist() == want and o.dtype == torch.int32
+    with pytest.raises(ValueError):
+        utils.generate_jagged_offs(2, 100, device="cpu")
