@@ -169,6 +169,45 @@ __device__ __forceinline__ void issue_tiles(uint8_t* sb, const Operand& X, const
   }
 }
 
+// Branch-free variant used by the pipelined loop: every load is range-checked
+// with a select, so a step outside [lo, hi) (e.g. a prefetch past the last
+// step) only writes zeros into the stage.
+template <class C>
+__device__ __forceinline__ void issue_tiles_sel(uint8_t* sb, const Operand& X, const Operand& W,
+                                                const LoadPlan<C>& P, int st, int lo, int hi) {
+  const int wave = wave_id();
+  const uint32_t xso = (uint32_t)st * C::XROW;
+  const uint32_t wso = (uint32_t)st * C::WROW;
+  const int kk = st * BK;
+  constexpr int WCH = C::WFMT == MXGG_FMT_E2M1 ? 32 : 16;
+#pragma unroll
+  for (int i = 0; i < C::QX; ++i) {
+    const int k = kk + P.xk[i];
+    const uint32_t off = (k >= lo && k + 16 <= hi) ? P.xoff[i] : kOOB;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(X.data, (lds_ptr_t)(sb + (wave * C::QX + i) * 1024), 16,
+                                             off, xso, 0, 0);
+  }
+  uint8_t* wb = sb + C::XBYTES;
+#pragma unroll
+  for (int i = 0; i < C::QW; ++i) {
+    const int k = kk + P.wk[i];
+    const uint32_t off = (k >= lo && k + WCH <= hi) ? P.woff[i] : kOOB;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(W.data, (lds_ptr_t)(wb + (wave * C::QW + i) * 1024), 16,
+                                             off, wso, 0, 0);
+  }
+}
+
+// Byte mask (0xff per 32-element block) of the step's blocks outside [lo, hi).
+__device__ __forceinline__ uint32_t outside_mask(int st, int lo, int hi) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int k = st * BK + 32 * b;
+    m |= (k < lo || k >= hi) ? (0xffu << (8 * b)) : 0u;
+  }
+  return m;
+}
+
 // Scale dwords of step `st`: byte b = scale of the 32-element block 4*st + b.
 template <bool DW>
 __device__ __forceinline__ uint32_t load_scale4(__amdgpu_buffer_rsrc_t r, uint32_t off, int st) {
@@ -257,6 +296,10 @@ __device__ __forceinline__ void mma_half(const uint8_t* sb, const uint32_t (&xs)
 // All of this wave's LDS reads have returned, then barrier: the stage may be
 // overwritten by any wave afterwards.
 #define MXGG_RELEASE() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+// Padding that lets in-flight v_mfma_scale instructions read their operands
+// before the registers can be rewritten: the compiler does not model the
+// scale operands as in-flight reads.
+#define MXGG_MFMA_DRAIN() asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory")
 
 // Reduction over steps [s0, s1) (global 128-element steps) restricted to the
 // element range [lo, hi).  Steps that are not fully inside [lo, hi) are masked.
@@ -323,6 +366,7 @@ __device__ __forceinline__ void mainloop(uint8_t* smem, const Operand& X, const 
     mma_half<C, 0>(sb, xsh, wsh, acc);
     mma_half<C, 1>(sb, xsh, wsh, acc);
     MXGG_RELEASE();
+    MXGG_MFMA_DRAIN();
     if constexpr (!DW) {
 #pragma unroll
       for (int i = 0; i < C::FM; ++i) xc[i] = xn[i];
@@ -330,6 +374,242 @@ __device__ __forceinline__ void mainloop(uint8_t* smem, const Operand& X, const 
       for (int j = 0; j < C::FN; ++j) wc[j] = wn_[j];
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Software-pipelined main loop (aligned-scale path).
+//
+// Per 128-element step s (stage s%2 holds step s, step s+1 is in flight):
+//   half 0: multiply fragments Fa (k 0..63) while the k 64..127 fragments of
+//           the same step are read into Fb;
+//   half 1: issue two MFMAs on Fb, then -- while they run -- wait for step
+//           s+1 to land, take the workgroup barrier (the one barrier of the
+//           step), read step s+1's scales and k 0..63 fragments into Fa,
+//           start the global->LDS copies of step s+2 into the stage just
+//           released, and issue the remaining MFMAs on Fb.
+// Every wave has finished reading stage s%2 (lgkmcnt(0)) before that barrier,
+// so after it the stage can be refilled.
+// ---------------------------------------------------------------------------
+
+template <class C>
+struct Frags {
+  v8i a[C::FN];   // W fragments (MFMA A operand)
+  v8i b[C::FM];   // X fragments (MFMA B operand)
+};
+
+template <class C, int H>
+__device__ __forceinline__ void read_frags(const uint8_t* sb, Frags<C>& F) {
+  const int wave = wave_id();
+  const int lane = threadIdx.x % kWave;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int hsel = lane >> 5;
+  const int r32 = lane & 31;
+  const int sw8 = swz8(r32);
+  const int c0 = (4 * H + hsel) ^ sw8;
+  const int c1 = (4 * H + 2 + hsel) ^ sw8;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+    const uint8_t* row = sb + (wm * C::WTM + i * 32 + r32) * C::XROW;
+    v4i lo = *reinterpret_cast<const v4i*>(row + c0 * 16);
+    v4i hi = *reinterpret_cast<const v4i*>(row + c1 * 16);
+    F.b[i] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  const uint8_t* wb = sb + C::XBYTES;
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const uint8_t* row = wb + (wn * C::WTN + j * 32 + r32) * C::WROW;
+    if constexpr (C::WFMT == MXGG_FMT_E2M1) {
+      const int c = (2 * H + hsel) ^ swz4(r32);
+      v4i lo = *reinterpret_cast<const v4i*>(row + c * 16);
+      F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
+    } else {
+      v4i lo = *reinterpret_cast<const v4i*>(row + c0 * 16);
+      v4i hi = *reinterpret_cast<const v4i*>(row + c1 * 16);
+      F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  }
+}
+
+// Scale dwords of the step in stage `sb`, shifted so that op_sel 2*H picks
+// the byte of the lane's 32-element block; blocks outside [lo, hi) neutral.
+template <class C>
+__device__ __forceinline__ void read_scales_raw(const uint8_t* sb, uint32_t (&xs)[C::FM],
+                                                uint32_t (&ws)[C::FN]) {
+  const int wave = wave_id();
+  const int lane = threadIdx.x % kWave;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+    xs[i] = *reinterpret_cast<const uint32_t*>(sb + C::XSOFF + (wm * C::WTM + i * 32 + (lane & 31)) * 4);
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j)
+    ws[j] = *reinterpret_cast<const uint32_t*>(sb + C::WSOFF + (wn * C::WTN + j * 32 + (lane & 31)) * 4);
+}
+
+// Neutralize the blocks of step st outside [lo, hi) and shift so that op_sel
+// 2*H picks the byte of the lane's 32-element block.
+template <class C>
+__device__ __forceinline__ void finish_scales(uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN], int st,
+                                              int lo, int hi) {
+  const int sh = 8 * ((threadIdx.x % kWave) >> 5);
+  const uint32_t m = outside_mask(st, lo, hi);        // wave-uniform
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) xs[i] = ((xs[i] & ~m) | (0x7f7f7f7fu & m)) >> sh;
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) ws[j] = ((ws[j] & ~m) | (0x7f7f7f7fu & m)) >> sh;
+}
+
+// MFMAs number [B, E) of the half's FM x FN grid (row-major over (i, j)).
+template <class C, int H, int B, int E>
+__device__ __forceinline__ void mfma_range(const Frags<C>& F, const uint32_t (&xs)[C::FM],
+                                           const uint32_t (&ws)[C::FN], v16f (&acc)[C::FM][C::FN]) {
+#pragma unroll
+  for (int t = B; t < E; ++t) {
+    const int i = t / C::FN, j = t % C::FN;
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+        F.a[j], F.b[i], acc[i][j], C::WFMT, MXGG_FMT_E4M3, 2 * H, (int)ws[j], 2 * H, (int)xs[i]);
+  }
+}
+
+template <class C>
+__device__ __forceinline__ void issue_step(uint8_t* sb, const Operand& X, const Operand& W,
+                                           const LoadPlan<C>& P, int st, int lo, int hi) {
+  issue_tiles_sel<C>(sb, X, W, P, st, lo, hi);
+  issue_scales<C>(sb, X, W, P, st);
+}
+
+// Keep the MFMA operand registers of a region allocated until the region's
+// end.  The compiler does not guard the scale operands of v_mfma_scale_* as
+// in-flight reads, so a register freed by an MFMA's last use could otherwise be
+// rewritten by the very next VALU instruction while the MFMA still reads it.
+template <class FR, int NM, int NN>
+__device__ __forceinline__ void hold(const FR& F, const uint32_t (&xs)[NM], const uint32_t (&ws)[NN]) {
+#if defined(__HIP_DEVICE_COMPILE__)   // VGPR constraints exist only in the device pass
+#pragma unroll
+  for (int i = 0; i < NM; ++i) asm volatile("" ::"v"(xs[i]), "v"(F.b[i]));
+#pragma unroll
+  for (int j = 0; j < NN; ++j) asm volatile("" ::"v"(ws[j]), "v"(F.a[j]));
+#endif
+}
+
+#define MXGG_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// Scheduling recipe for one region: NM MFMAs with NV VMEM reads and ND DS
+// reads spread evenly between them (sched_group_barrier groups, in order).
+template <int I, int NM, int NV, int ND>
+__device__ __forceinline__ void interleave_step() {
+  if constexpr (I < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // 1 MFMA
+    constexpr int v = (NV * (I + 1)) / NM - (NV * I) / NM;
+    constexpr int d = (ND * (I + 1)) / NM - (ND * I) / NM;
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);   // VMEM (incl. LDS DMA)
+    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);   // DS reads
+    interleave_step<I + 1, NM, NV, ND>();
+  }
+}
+
+template <int NM, int NV, int ND>
+__device__ __forceinline__ void interleave() {
+  interleave_step<0, NM, NV, ND>();
+}
+
+// One steady-state step st (a next step exists).  Scales of step st are in
+// (xs, ws); step st+1's are produced into (xn, wn).  The step ends with a drain
+// so that the caller may then overwrite (xs, ws).
+template <class C>
+__device__ __forceinline__ void pipe_step(uint8_t* smem, const Operand& X, const Operand& W,
+                                          const LoadPlan<C>& P, int s0, int st, int lo, int hi,
+                                          Frags<C>& Fa, Frags<C>& Fb, uint32_t (&xs)[C::FM],
+                                          uint32_t (&ws)[C::FN], uint32_t (&xn)[C::FM],
+                                          uint32_t (&wn)[C::FN], v16f (&acc)[C::FM][C::FN]) {
+  constexpr int NMMA = C::FM * C::FN;
+  constexpr int NEARLY = NMMA >= 8 ? 2 : 1;    // MFMAs of half 1 issued before the barrier
+  constexpr int NDS0 = C::FM * 2 + (C::WFMT == MXGG_FMT_E2M1 ? C::FN : C::FN * 2);
+  const int cur = (st - s0) & 1;
+  uint8_t* sb = smem + cur * C::STAGE;
+  uint8_t* nb = smem + (cur ^ 1) * C::STAGE;
+  // ---- half 0: MFMAs on Fa, reads of the second half into Fb in between
+  read_frags<C, 1>(sb, Fb);
+  mfma_range<C, 0, 0, NMMA>(Fa, xs, ws, acc);
+  interleave<NMMA, 0, NDS0>();
+  MXGG_SCHED_FENCE();
+  hold(Fa, xs, ws);
+  // ---- half 1
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  mfma_range<C, 1, 0, NEARLY>(Fb, xs, ws, acc);
+  MXGG_SCHED_FENCE();
+  MXGG_WAIT_VM(0);
+  MXGG_BARRIER();
+  MXGG_SCHED_FENCE();
+  // step st+1's scales and first-half fragments are read before the copies of
+  // step st+2 are issued into the stage just released (past the end: zeros,
+  // never read).  Reads issued in between those LDS-DMA loads came back
+  // corrupted when the compiler gave a read a destination register that a
+  // just-issued DMA load used as its offset.
+  read_scales_raw<C>(nb, xn, wn);
+  read_frags<C, 0>(nb, Fa);
+  issue_step<C>(sb, X, W, P, st + 2, lo, hi);
+  mfma_range<C, 1, NEARLY, NMMA>(Fb, xs, ws, acc);
+  MXGG_SCHED_FENCE();
+  hold(Fb, xs, ws);
+  MXGG_MFMA_DRAIN();
+  MXGG_SCHED_FENCE();
+  finish_scales<C>(xn, wn, st + 1, lo, hi);
+}
+
+template <class C>
+__device__ __forceinline__ void pipe_last(const uint8_t* sb, Frags<C>& Fa, Frags<C>& Fb,
+                                          const uint32_t (&xs)[C::FM], const uint32_t (&ws)[C::FN],
+                                          v16f (&acc)[C::FM][C::FN]) {
+  constexpr int NMMA = C::FM * C::FN;
+  read_frags<C, 1>(sb, Fb);
+  mfma_range<C, 0, 0, NMMA>(Fa, xs, ws, acc);
+  mfma_range<C, 1, 0, NMMA>(Fb, xs, ws, acc);
+  MXGG_SCHED_FENCE();
+  hold(Fa, xs, ws);
+  hold(Fb, xs, ws);
+  MXGG_MFMA_DRAIN();
+  MXGG_SCHED_FENCE();
+}
+
+template <class C>
+__device__ __forceinline__ void mainloop_pipe(uint8_t* smem, const Operand& X, const Operand& W,
+                                              int s0, int s1, int lo, int hi,
+                                              v16f (&acc)[C::FM][C::FN]) {
+  if (s0 >= s1) return;
+  constexpr int NLOAD = C::QX + C::QW + C::QS;
+  LoadPlan<C> P;
+  make_plan<C>(P, X, W);
+
+  issue_step<C>(smem, X, W, P, s0, lo, hi);
+  if (s0 + 1 < s1) {
+    issue_step<C>(smem + C::STAGE, X, W, P, s0 + 1, lo, hi);
+    MXGG_WAIT_VM(NLOAD);
+  } else {
+    MXGG_WAIT_VM(0);
+  }
+  MXGG_BARRIER();
+  Frags<C> Fa, Fb;
+  uint32_t xa[C::FM], wa[C::FN], xb[C::FM], wb[C::FN];
+  read_scales_raw<C>(smem, xa, wa);
+  read_frags<C, 0>(smem, Fa);
+  finish_scales<C>(xa, wa, s0, lo, hi);
+
+  // steady state: a next step always exists
+  int st = s0;
+  for (; st + 1 < s1; ++st) {
+    pipe_step<C>(smem, X, W, P, s0, st, lo, hi, Fa, Fb, xa, wa, xb, wb, acc);
+    // xb/wb now hold step st+1's scales; move them into the current set only
+    // after the step's last MFMAs have read xa/wa (pipe_step ends with a drain)
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) xa[i] = xb[i];
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) wa[j] = wb[j];
+  }
+  pipe_last<C>(smem + ((st - s0) & 1) * C::STAGE, Fa, Fb, xa, wa, acc);
+  // the zero-filled prefetch past the last step may still be writing LDS:
+  // drain it before the workgroup can exit and its LDS be reallocated
+  MXGG_WAIT_VM(0);
 }
 
 // Store an accumulator tile.  Lane l of fragment (i, j) holds output row
@@ -442,7 +722,8 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 
   const int K = (int)p.K;
-  mainloop<C, DW>(smem, X, W, 0, (K + BK - 1) / BK, 0, K, acc);
+  if constexpr (DW) mainloop_pipe<C>(smem, X, W, 0, (K + BK - 1) / BK, 0, K, acc);
+  else mainloop<C, DW>(smem, X, W, 0, (K + BK - 1) / BK, 0, K, acc);
 
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   store_tile<C, false>(acc, p.out + (row0 * p.ldo + n0) * esz, p.ldo, rows, cols, p.out_dtype);
@@ -491,7 +772,10 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 
-  if (hi > lo) mainloop<C, DW>(smem, X, W, lo / BK, (hi + BK - 1) / BK, lo, hi, acc);
+  if (hi > lo) {
+    if constexpr (DW) mainloop_pipe<C>(smem, X, W, lo / BK, (hi + BK - 1) / BK, lo, hi, acc);
+    else mainloop<C, DW>(smem, X, W, lo / BK, (hi + BK - 1) / BK, lo, hi, acc);
+  }
 
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
@@ -553,9 +837,9 @@ using namespace mxgg;
 
 namespace {
 
-typedef Cfg<256, 256, 2, 4, MXGG_FMT_E4M3> CfgF8_256;
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3> CfgF8_256;
 typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3> CfgF8_128;
-typedef Cfg<256, 256, 2, 4, MXGG_FMT_E2M1> CfgF4_256;
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1> CfgF4_256;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
