@@ -64,6 +64,100 @@ def time_call(fn, steps: int, warmup: int, flush_buf):
     return statistics.median(ts), sum(ts) / len(ts)
 
 
+def fwd_kernel_name(cfg: dict) -> str:
+    """Device-kernel name (as rocprofv3 lists it) of a forward/dgrad launch."""
+    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0>, true>"
+
+
+def read_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (profiles/hbm_traffic_sweep.txt, lines `traffic_bytes_per_launch <kernel> = <bytes>`),
+    or None when no measurement of that kernel is recorded."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_sweep.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch ") and "=" in line:
+            name, val = line[len("traffic_bytes_per_launch "):].rsplit("=", 1)
+            if name.strip() == kernel:
+                return float(val)
+    return None
+
+
+def copy_calibration(dev, mib: int = 256, reps: int = 3):
+    """A plain device copy of known size, run so that a PMC pass over this
+    program can scale FETCH_SIZE / WRITE_SIZE (the copy moves mib MiB each way)."""
+    import torch
+    src = torch.empty(mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {reps} copies of {mib} MiB")
+    del src, dst
+
+
+def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shapes: int) -> str:
+    """HBM bytes per launch of each GEMM kernel from two rocprofv3 --pmc passes
+    (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) over
+    ``bench.py --steps S --warmup W --no-cpu --copy-calibration``.
+
+    Each counter is scaled so that the calibration copy (256 MiB each way)
+    reads 256 MiB; dispatches are matched to sweep shapes by launch order
+    (per shape: fwd, dgrad, wgrad, each warmup + steps launches) to set the
+    algorithmic bytes beside the measured ones."""
+    import csv
+
+    def load(path, counter):
+        rows = [(int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]))
+                for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        return sorted(rows)
+
+    out = []
+    scaled = {}
+    for path, counter in ((fetch_csv, "FETCH_SIZE"), (write_csv, "WRITE_SIZE")):
+        rows = load(path, counter)
+        cal = [v for _, n, v in rows[:64] if "copyBuffer" in n and v > 1e4][:3]
+        if len(cal) != 3:
+            raise SystemExit(f"{path}: calibration copies not found")
+        factor = (256 * 1024.0) / (sum(cal) / 3)
+        out.append(f"{counter}: calibration copy reads {sum(cal) / 3:.1f} KiB per 256 MiB copy -> "
+                   f"scale factor {factor:.4f}")
+        scaled[counter] = [(n, v * factor * 1024.0) for _, n, v in rows if "mxgg::" in n and "_kernel<" in n
+                           and "quant" not in n]
+    f, w = scaled["FETCH_SIZE"], scaled["WRITE_SIZE"]
+    per = warmup + steps
+    shapes = SHAPES[:n_shapes]
+    want = []
+    for (e, n, k) in shapes:
+        for kind in ("fwd", "dgrad", "wgrad"):
+            if kind == "wgrad":
+                alg = (n + k) * M_TOKENS * (1 + 1 / 32) + 2 * e * n * k
+            else:
+                nn, kk = (n, k) if kind == "fwd" else (k, n)
+                alg = M_TOKENS * kk * (1 + 1 / 32) + e * nn * kk * (1 + 1 / 32) + 2 * M_TOKENS * nn
+            want += [(kind, alg)] * per
+    if not (len(f) == len(w) == len(want)):
+        raise SystemExit(f"dispatch count mismatch: fetch {len(f)}, write {len(w)}, expected {len(want)}")
+    agg = {}
+    for (nf, vf), (nw, vw), (kind, alg) in zip(f, w, want):
+        assert nf == nw and (("wgrad" in nf) == (kind == "wgrad")), (nf, nw, kind)
+        name = nf.replace("void ", "").split("(")[0]
+        a = agg.setdefault(name, [0.0, 0.0, 0.0, 0])
+        a[0] += vf
+        a[1] += vw
+        a[2] += alg
+        a[3] += 1
+    out.append(f"{'kernel':58s} {'launches':>8s} {'fetch MB':>9s} {'write MB':>9s} {'total MB':>9s} "
+               f"{'algorithmic MB':>14s} {'ratio':>6s}")
+    for name, (vf, vw, alg, c) in sorted(agg.items()):
+        out.append(f"{name:58s} {c:8d} {vf / c / 1e6:9.1f} {vw / c / 1e6:9.1f} {(vf + vw) / c / 1e6:9.1f} "
+                   f"{alg / c / 1e6:14.1f} {(vf + vw) / alg:6.2f}")
+    for name, (vf, vw, alg, c) in sorted(agg.items()):
+        out.append(f"traffic_bytes_per_launch {name} = {(vf + vw) / c:.0f}")
+    return "\n".join(out)
+
+
 def geomean(xs):
     return math.exp(sum(math.log(x) for x in xs) / len(xs))
 
@@ -112,7 +206,16 @@ def main():
     ap.add_argument("--shapes", type=int, default=36, help="first N shapes of the sweep")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 plain 256 MiB device copies (PMC byte-counter calibration)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarize two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of "
+                         "`bench.py --steps S --warmup W --no-cpu --copy-calibration` (same S, W, --shapes) "
+                         "and exit; runs on the CPU")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.steps, args.warmup, args.shapes))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -121,6 +224,7 @@ def main():
     import torch
     import kernels
     from kernels import to_mx, to_mx_dim0, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
+    from kernels.forward import _pick_config
     from utils import generate_jagged_offs
 
     if not kernels._rocm_mxfp8_available or not torch.cuda.is_available():
@@ -131,11 +235,19 @@ def main():
     flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.int32, device=dev)
     shapes = SHAPES[: args.shapes]
     offs_by_shape = {s: generate_jagged_offs(s[0], M_TOKENS, multiple_of=32, device=dev) for s in shapes}
+    if args.copy_calibration:
+        copy_calibration(dev)
 
     rows = []
-    kernel_ms = {"fwd": 0.0, "dgrad": 0.0}
-    kernel_flops = {"fwd": 0.0, "dgrad": 0.0}
-    kernel_launches = {"fwd": 0, "dgrad": 0}
+    # per device kernel: summed event time (ms), FLOPs and launches of the timed reps
+    kstats = {}
+
+    def account(kernel, mean_ms, flops):
+        k = kstats.setdefault(kernel, {"ms": 0.0, "flops": 0.0, "launches": 0})
+        k["ms"] += mean_ms * args.steps
+        k["flops"] += flops * args.steps
+        k["launches"] += args.steps
+
     t_start = time.time()
     for (E, N, K) in shapes:
         M = M_TOKENS
@@ -152,9 +264,7 @@ def main():
                                   args.steps, args.warmup, flush)
             row["fwd_us"] = med * 1e3
             row["fwd_tflops"] = flops / (med * 1e-3) / 1e12
-            kernel_ms["fwd"] += mean * args.steps
-            kernel_flops["fwd"] += flops * args.steps
-            kernel_launches["fwd"] += args.steps
+            account(fwd_kernel_name(_pick_config(E, M, N, K)), mean, flops)
             del qa, qw, sa, sw
         if args.only in ("all", "dgrad"):
             go = torch.randn((M, N), device=dev).to(torch.bfloat16)
@@ -166,9 +276,7 @@ def main():
                                   args.steps, args.warmup, flush)
             row["dgrad_us"] = med * 1e3
             row["dgrad_tflops"] = flops / (med * 1e-3) / 1e12
-            kernel_ms["dgrad"] += mean * args.steps
-            kernel_flops["dgrad"] += flops * args.steps
-            kernel_launches["dgrad"] += args.steps
+            account(fwd_kernel_name(_pick_config(E, M, K, N)), mean, flops)
             del qg, qt, sg, st_
         if args.only in ("all", "wgrad"):
             go = torch.randn((M, N), device=dev).to(torch.bfloat16)
@@ -176,10 +284,11 @@ def main():
             sg, qg = to_mx_dim0(go)          # (N, M)
             si, qi = to_mx_dim0(ia)          # (K, M)
             del go, ia
-            med, _ = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs),
-                               args.steps, args.warmup, flush)
+            med, mean = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs),
+                                  args.steps, args.warmup, flush)
             row["wgrad_us"] = med * 1e3
             row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
+            account("mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0>, true>", mean, flops)
             del qg, qi, sg, si
         torch.cuda.empty_cache()
         rows.append(row)
@@ -197,18 +306,21 @@ def main():
         if v:
             per_e[str(e)] = round(geomean(v), 1)
 
-    # roofline of the dominant kernel (the grouped GEMM kernel, fwd + dgrad launches)
-    kms = kernel_ms["fwd"] + kernel_ms["dgrad"]
-    kfl = kernel_flops["fwd"] + kernel_flops["dgrad"]
-    nl = kernel_launches["fwd"] + kernel_launches["dgrad"]
-    achieved = kfl / (kms * 1e-3) / 1e12 if kms else None
-    roofline = {"bound": "mfma", "achieved": round(achieved, 1) if achieved else None,
-                "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4) if achieved else None,
-                "traffic": None,
-                "kernel": "mxgg::fwd_kernel (forward + dgrad launches of the sweep)",
-                "avg_launch_us": round(kms / nl * 1e3, 2) if nl else None,
-                "launches": nl}
+    # roofline of the dominant device kernel (largest summed time over the timed
+    # reps): algorithmic FLOPs 2*M*N*K per launch / its mean launch duration
+    roofline = None
+    if kstats:
+        kname, k = max(kstats.items(), key=lambda kv: kv[1]["ms"])
+        achieved = k["flops"] / (k["ms"] * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MXFP8_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4),
+                    "traffic": read_traffic(kname), "kernel": kname,
+                    "avg_launch_us": round(k["ms"] / k["launches"] * 1e3, 2),
+                    "flops_per_launch": round(k["flops"] / k["launches"]),
+                    "launches": k["launches"],
+                    "by_kernel": {n: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 2),
+                                      "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
+                                      "launches": v["launches"]} for n, v in kstats.items()}}
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
     value = fwd_gm if fwd_gm is not None else (dgrad_gm or wgrad_gm)

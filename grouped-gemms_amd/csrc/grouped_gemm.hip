@@ -16,11 +16,13 @@
 //   * LDS rows are 128 bytes (e4m3) or 64 bytes (packed e2m1) with 16-byte
 //     chunks XOR-swizzled by row so the 32-row fragment reads are free of bank
 //     conflicts for both 8- and 16-lane LDS service groups.
-//   * two LDS stages (double buffering): the loads of step s+1 are in flight
-//     while step s is multiplied.
-//   * e8m0 scales are read straight from the plain `to_mx` layout with one
-//     dword buffer load per 32-row fragment and step (4 scale bytes = the 4
-//     32-element blocks of the step), and selected per MFMA with op_sel.
+//   * two LDS stages (double buffering) and a software-pipelined loop with
+//     one workgroup barrier per step (mainloop_pipe below).
+//   * e8m0 scales are read straight from the plain `to_mx` layout: one dword
+//     per tile row and step (the 4 scale bytes of the step's 4 32-element
+//     blocks) travels global -> LDS next to the data, and each MFMA selects
+//     its byte with op_sel.  Scale rows that are not 4-byte aligned take a
+//     byte-gather register path (mainloop below).
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
@@ -673,6 +675,89 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[C::FM][C::FN], uint
   }
 }
 
+// Store a 16-bit (bf16 / f16) accumulator tile through LDS so that every
+// global store instruction writes whole row segments: each wave transposes its
+// WTM x WTN tile into its own LDS area (rows of WTN*2 bytes, 16-byte chunks
+// XOR-swizzled by row), then 64 lanes store 64 consecutive 16-byte chunks
+// (WTN*2/16 chunks per row).  Tiles larger than the free LDS go in passes of
+// whole 32-row fragment rows.  Requires ldo % 8 == 0 and a 16-byte aligned
+// `out`; the caller must have drained every LDS-DMA load and the workgroup
+// must be past its last main-loop LDS read (this function begins with a
+// workgroup barrier).
+// Largest divisor of fm not above lim (fragment rows per staging pass).
+constexpr int store_pass_rows(int fm, int lim) {
+  int best = 1;
+  for (int d = 1; d <= fm; ++d)
+    if (fm % d == 0 && d <= lim) best = d;
+  return best;
+}
+
+template <class C>
+__device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], uint8_t* smem,
+                                               uint8_t* out, int64_t ldo, int rows, int cols,
+                                               int out_dtype) {
+  constexpr int RB = C::WTN * 2;                 // staged row bytes
+  constexpr int NCH = RB / 16;                   // 16-byte chunks per row
+  constexpr int AVAIL = 2 * C::STAGE / C::NW;    // LDS bytes per wave
+  constexpr int FPP = store_pass_rows(C::FM, AVAIL / (32 * RB));   // fragment rows per pass
+  static_assert(FPP >= 1 && C::FM % FPP == 0, "store staging");
+  static_assert(64 % NCH == 0, "store row width");
+  const int wave = wave_id();
+  const int lane = threadIdx.x % kWave;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  uint8_t* area = smem + wave * (FPP * 32 * RB);
+#pragma unroll
+  for (int i0 = 0; i0 < C::FM; i0 += FPP) {
+    __syncthreads();
+#pragma unroll
+    for (int ii = 0; ii < FPP; ++ii) {
+      const int m = ii * 32 + (lane & 31);
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const v16f& a = acc[i0 + ii][j];
+          uint32_t w0, w1;
+          if (out_dtype == MXGG_DTYPE_BF16) {
+            w0 = pack_bf16x2(a[4 * q4 + 0], a[4 * q4 + 1]);
+            w1 = pack_bf16x2(a[4 * q4 + 2], a[4 * q4 + 3]);
+          } else {
+            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+            h2 x = {(_Float16)a[4 * q4 + 0], (_Float16)a[4 * q4 + 1]};
+            h2 y = {(_Float16)a[4 * q4 + 2], (_Float16)a[4 * q4 + 3]};
+            w0 = __builtin_bit_cast(uint32_t, x);
+            w1 = __builtin_bit_cast(uint32_t, y);
+          }
+          const int c = 4 * j + q4;                      // 16-byte chunk (8 columns)
+          *reinterpret_cast<uint2*>(area + m * RB + ((c ^ (m % NCH)) * 16) + 8 * (lane >> 5)) =
+              make_uint2(w0, w1);
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int RPI = 64 / NCH;                        // rows per read instruction
+#pragma unroll
+    for (int it = 0; it < FPP * 32 / RPI; ++it) {
+      const int r = it * RPI + lane / NCH;
+      const int c = lane % NCH;
+      const uint4 v = *reinterpret_cast<const uint4*>(area + r * RB + ((c ^ (r % NCH)) * 16));
+      const int row = wm * C::WTM + i0 * 32 + r;
+      const int col = wn * C::WTN + c * 8;
+      if (row < rows) {
+        uint16_t* p = reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + col;
+        if (col + 8 <= cols) {
+          *reinterpret_cast<uint4*>(p) = v;
+        } else {
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (col + e < cols) p[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // forward / dgrad
 // ---------------------------------------------------------------------------
@@ -726,7 +811,11 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
   else mainloop<C, DW>(smem, X, W, 0, (K + BK - 1) / BK, 0, K, acc);
 
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-  store_tile<C, false>(acc, p.out + (row0 * p.ldo + n0) * esz, p.ldo, rows, cols, p.out_dtype);
+  uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
+  if (DW && esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
+    store_tile_lds<C>(acc, smem, o, p.ldo, rows, cols, p.out_dtype);
+  else
+    store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -779,7 +868,10 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
-  store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
+  if (DW && esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
+    store_tile_lds<C>(acc, smem, o, p.K, rows, cols, p.out_dtype);
+  else
+    store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -963,6 +1055,24 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   if (c.bm == 128 && c.bn == 128)
     return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, dw, st);
   return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built (256x256, 128x128)", c.bm, c.bn);
+}
+
+extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,
+                                      int* block_n, int* group_m, int* xcd_swizzle) {
+  clear_error();
+  if (!block_m || !block_n || !group_m || !xcd_swizzle)
+    return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_config: null output pointer");
+  if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
+    return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_config: weight format %d not E4M3/E2M1", b_fmt);
+  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, *block_m, *block_n, *group_m, *xcd_swizzle);
+  *block_m = c.bm;
+  *block_n = c.bn;
+  *group_m = c.group_m;
+  *xcd_swizzle = c.xcd;
+  const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
+                                           : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
+  if (!built) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm_config: tile %dx%d not built", c.bm, c.bn);
+  return MXGG_OK;
 }
 
 extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K) {

@@ -52,6 +52,9 @@ SIGNATURES = {
                                  _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
                                  _c_p, _c_i32, _c_i64,
                                  _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
+    "mxgg_grouped_mm_config": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32,
+                                        ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32),
+                                        ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32)]),
     "mxgg_wgrad_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
     "mxgg_wgrad": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
                             _c_p, _c_i64, _c_p, _c_i64,

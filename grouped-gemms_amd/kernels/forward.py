@@ -25,6 +25,25 @@ BUILT_TILES = ((256, 256), (128, 128))
 _FP4_DTYPES = tuple(d for d in (getattr(torch, "float4_e2m1fn_x2", None), torch.uint8) if d is not None)
 
 
+def _pick_config(E: int, M: int, N: int, K: int, b_fmt: int = _lib.FMT_E4M3, BLOCK_M: int = 0,
+                 BLOCK_N: int = 0, GROUP_M: int = 0, XCD_SWIZZLE: int = 0) -> dict:
+    """Launch configuration of one grouped-GEMM call (kernels/forward.py:399-459).
+
+    The reference looks ``(E, N, K)`` up in a table of Triton meta-parameters;
+    here libmxgg owns the table (``mxgg_grouped_mm_config``) so that C callers
+    get the same choice.  Returns ``{"BLOCK_M", "BLOCK_N", "BLOCK_K",
+    "GROUP_M", "XCD_SWIZZLE"}``; requested values are applied when the tile is
+    built (``MXGGError`` with code MXGG_ERR_UNSUPPORTED otherwise).
+    """
+    import ctypes
+    bm, bn, gm, xcd = (ctypes.c_int(int(v or 0)) for v in (BLOCK_M, BLOCK_N, GROUP_M, XCD_SWIZZLE))
+    rc = _lib.load().mxgg_grouped_mm_config(int(E), int(M), int(N), int(K), int(b_fmt), ctypes.byref(bm),
+                                            ctypes.byref(bn), ctypes.byref(gm), ctypes.byref(xcd))
+    _lib.check(rc)
+    return {"BLOCK_M": bm.value, "BLOCK_N": bn.value, "BLOCK_K": 128, "GROUP_M": gm.value,
+            "XCD_SWIZZLE": xcd.value}
+
+
 def triton_mxfp8_grouped_mm(
     input_act: torch.Tensor,
     weight: torch.Tensor,

@@ -110,6 +110,18 @@ int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t N, int blo
                        int block_n, int group_m, int xcd_swizzle, int32_t* out, void* stream);
 
 /*
+ * Launch configuration the library uses for a grouped GEMM of this shape:
+ * tile (block_m x block_n; the reduction step is fixed at 128), GROUP_M and
+ * XCD swizzle width.  Requests (nonzero *block_m, *block_n, *group_m,
+ * *xcd_swizzle on entry) are applied as mxgg_grouped_mm applies them; the
+ * call returns MXGG_ERR_UNSUPPORTED when the resulting tile is not built.
+ * Replaces `_pick_config` / `_BEST_CFGS` / `_FALLBACK_*`
+ * (kernels/forward.py:399-459).
+ */
+int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,
+                           int* block_n, int* group_m, int* xcd_swizzle);
+
+/*
  * Forward / dgrad grouped GEMM: out[s:e, :] = A[s:e, :] @ B[g]^T for each group
  * g with rows [offs[g-1], offs[g]) (offs[-1] = 0), MX scales applied per 32
  * elements of K, fp32 accumulation, one rounding to out_dtype.

@@ -48,6 +48,24 @@ def test_pure_size_helpers():
     assert lib.mxgg_routing_words(0, 10, 128) == 0
 
 
+def test_launch_config_query():
+    """mxgg_grouped_mm_config (the counterpart of _pick_config) is pure host logic."""
+    from kernels import _lib
+    from kernels.forward import _pick_config
+    big = _pick_config(8, 16640, 8192, 8192)
+    assert (big["BLOCK_M"], big["BLOCK_N"], big["BLOCK_K"]) == (256, 256, 128)
+    assert big["GROUP_M"] > 0 and big["XCD_SWIZZLE"] == 8
+    small = _pick_config(1, 16640, 2048, 2048)
+    assert (small["BLOCK_M"], small["BLOCK_N"]) == (128, 128)
+    assert _pick_config(1, 16640, 2048, 2048, b_fmt=_lib.FMT_E2M1)["BLOCK_M"] == 256
+    req = _pick_config(1, 16640, 8192, 8192, BLOCK_M=128, BLOCK_N=128, GROUP_M=4, XCD_SWIZZLE=1)
+    assert (req["BLOCK_M"], req["BLOCK_N"], req["GROUP_M"], req["XCD_SWIZZLE"]) == (128, 128, 4, 1)
+    with pytest.raises(_lib.MXGGError):
+        _pick_config(1, 16640, 2048, 2048, b_fmt=_lib.FMT_E2M1, BLOCK_M=128, BLOCK_N=128)
+    with pytest.raises(ValueError):
+        _pick_config(1, 16640, 2048, 2048, b_fmt=3)
+
+
 @pytest.mark.parametrize("args,needle", [
     (dict(b_fmt=3), "weight format"),
     (dict(out_dtype=9), "out_dtype"),
