@@ -2,6 +2,7 @@
 //   * forward / dgrad:  out[s:e] = A[s:e] @ B[g]^T          (kernels/forward.py:81-294)
 //   * weight gradient:  out[g]   = GO[:, s:e] @ IA[:, s:e]^T (kernels/backward.py:31-215)
 //   * routing table and tile schedule exposed for testing   (kernels/forward.py:31-51, 296-365)
+//   * scale re-layout feeding both GEMMs                    (the role of kernels/forward.py:367-397)
 //
 // Both GEMMs are "NT" products whose two operands are contiguous along the
 // reduction dimension, so they share one main loop:
@@ -9,389 +10,95 @@
 // with X on the B side and W on the A side of v_mfma_scale_f32_32x32x64_f8f6f4,
 // so that every lane of the accumulator holds 4 consecutive output columns.
 //
-// Main loop per 128-element reduction step (BK = 128):
-//   * X and W tiles go global -> LDS directly with 16-byte buffer_load ... lds
-//     (no VGPR staging); rows past the valid range and masked reduction chunks
-//     read as zero through the buffer range check.
-//   * LDS rows are 128 bytes (e4m3) or 64 bytes (packed e2m1) with 16-byte
-//     chunks XOR-swizzled by row so the 32-row fragment reads are free of bank
-//     conflicts for both 8- and 16-lane LDS service groups.
-//   * two LDS stages (double buffering) and a software-pipelined loop with
-//     one workgroup barrier per step (mainloop_pipe below).
-//   * e8m0 scales are read straight from the plain `to_mx` layout: one dword
-//     per tile row and step (the 4 scale bytes of the step's 4 32-element
-//     blocks) travels global -> LDS next to the data, and each MFMA selects
-//     its byte with op_sel.  Scale rows that are not 4-byte aligned take a
-//     byte-gather register path (mainloop below).
+// Main loop (ring_mainloop): the reduction runs in 64-element stages held in
+// an NS-deep LDS ring.  While stage s is multiplied out of registers, stage
+// s+1 is read from LDS and stages s+2 .. s+NS are in flight, so the copies of
+// a stage have NS-1 stage times to land and the copy engine always has
+// several stages queued.  (An LDS-DMA copy costs about the same per
+// instruction whatever its row length, so shorter stages cost nothing extra
+// while deeper queues hide the memory latency.)
+//   * X and W tiles go global -> LDS directly with 16-byte buffer_load ... lds;
+//     chunks outside the reduction range read as zero through the buffer
+//     range check.  LDS rows are 64 bytes (e4m3) or 32 bytes (packed e2m1)
+//     with 16-byte chunks XOR-swizzled by row: conflict-free fragment reads.
+//   * e8m0 scales: a re-layout kernel first writes the plain `to_mx` scales
+//     step-major, one dword (4 scale bytes = one 128-element step) per row:
+//     [step][row].  The scales of a tile for two steps are then a few
+//     contiguous 1 KB pieces, copied into a two-slot scale ring every four
+//     stages; each MFMA takes its lane's byte at op_sel 0.
+//   * one workgroup barrier per stage; fragment and scale registers alternate
+//     between two sets (loop body unrolled twice).
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
 namespace mxgg {
 
-constexpr int BK = 128;
+constexpr int BKS = 64;        // reduction elements per stage
+constexpr int STEP = 128;      // reduction elements per scale dword (4 blocks of 32)
+constexpr int SCG = 2;         // steps per scale group (one scale-ring slot)
+constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
 
-template <int BM_, int BN_, int WGM_, int WGN_, int WFMT_>
+template <int BM_, int BN_, int WGM_, int WGN_, int WFMT_, int NS_>
 struct Cfg {
   static constexpr int BM = BM_;        // X rows per tile (output rows)
   static constexpr int BN = BN_;        // W rows per tile (output columns)
   static constexpr int WGM = WGM_;      // waves along rows
   static constexpr int WGN = WGN_;      // waves along columns
   static constexpr int WFMT = WFMT_;    // W element format (X is always e4m3)
+  static constexpr int NS = NS_;        // ring depth (stages)
+  static constexpr bool F4 = WFMT == MXGG_FMT_E2M1;
   static constexpr int NW = WGM * WGN;
   static constexpr int NT = NW * kWave;
   static constexpr int WTM = BM / WGM;
   static constexpr int WTN = BN / WGN;
   static constexpr int FM = WTM / 32;
   static constexpr int FN = WTN / 32;
-  static constexpr int XROW = BK;                                  // bytes per X row per step
-  static constexpr int WROW = WFMT == MXGG_FMT_E2M1 ? BK / 2 : BK;  // bytes per W row per step
+  static constexpr int XROW = BKS;                  // bytes per X row per stage
+  static constexpr int WROW = F4 ? BKS / 2 : BKS;   // bytes per W row per stage
   static constexpr int XBYTES = BM * XROW;
   static constexpr int WBYTES = BN * WROW;
-  static constexpr int XSOFF = XBYTES + WBYTES;                   // X scale dwords (BM x 4 B)
-  static constexpr int WSOFF = XSOFF + BM * 4;                     // W scale dwords (BN x 4 B)
-  static constexpr int STAGE = WSOFF + BN * 4;
-  static constexpr int QX = XBYTES / 1024 / NW;                   // 1 KB loads per wave
+  static constexpr int STAGE = XBYTES + WBYTES;
+  // scale ring after the data ring: two slots of SCG steps x (BM X rows, then
+  // BN W rows) dwords
+  static constexpr int SSLOT = SCG * (BM + BN) * 4;
+  static constexpr int SOFF = NS * STAGE;
+  static constexpr int LDS = SOFF + 2 * SSLOT;
+  static constexpr int QX = XBYTES / 1024 / NW;     // 1 KB data copies per wave and stage
   static constexpr int QW = WBYTES / 1024 / NW;
-  static constexpr int QS = (BM + BN) / 64 / NW;                   // 256 B scale loads per wave
+  static constexpr int LPS = QX + QW;               // LDS-DMA loads per wave and stage
+  static constexpr int NSD = SSLOT / 1024;          // 1 KB scale copies per group
   static_assert(XBYTES % (1024 * NW) == 0 && WBYTES % (1024 * NW) == 0, "tile/wave split");
-  static_assert((BM + BN) % (64 * NW) == 0 && BM % 64 == 0, "scale/wave split");
+  static_assert(SSLOT % 1024 == 0 && NSD <= NW, "scale copies: at most one per wave");
+  static_assert(BM % 4 == 0 && (BM + BN) % 4 == 0, "scale pieces stay in one operand and step");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  static_assert(NS >= 3 && LDS <= 160 * 1024, "ring depth / LDS budget");
+  // a scale group is copied SPG - 1 stages before its first read; the wait
+  // before that read covers it only if the stage read then was issued no
+  // earlier than the group
+  static_assert(NS <= SPG + 1, "ring deeper than the scale prefetch");
+  static_assert((NS - 1) * LPS <= 63, "vmcnt range");
 };
 
-// 16-byte chunk swizzles (see header comment): bijective on the chunk index for
-// every 8-row and every parity class of 16 rows (128-byte rows), resp. every
-// 4-row class of 8 and 16 rows (64-byte rows).
-__device__ __forceinline__ int swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+// 16-byte chunk swizzles: bijective on the chunk index for every 8-row and
+// every 16-row class, 64-byte rows (swz4) and 32-byte rows (swz2).  Both
+// depend on row % 16 only.
 __device__ __forceinline__ int swz4(int r) {
   return ((((r >> 2) ^ (r >> 3)) & 1) << 1) | (((r >> 1) ^ (r >> 2)) & 1);
 }
+__device__ __forceinline__ int swz2(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
 struct Operand {
   __amdgpu_buffer_rsrc_t data;   // base = first row of the tile; range = valid rows
-  __amdgpu_buffer_rsrc_t scale;  // base = scales of the first row; range = valid rows
   uint32_t ld;                   // bytes between rows
-  uint32_t lds;                  // scale bytes between rows
 };
 
-template <class C>
-struct LoadPlan {
-  uint32_t xoff[C::QX];     // per-lane byte offset of each 1 KB X load (row * ld + chunk)
-  uint32_t woff[C::QW];
-  int xk[C::QX];            // reduction element of the lane's X chunk inside the step
-  int wk[C::QW];
-  uint32_t xs_off[C::FM];   // per-lane scale row offsets (register path)
-  uint32_t ws_off[C::FN];
-  uint32_t s_off[C::QS];    // per-lane scale row offsets (LDS path, one row per lane)
+// Where a tile's re-laid scales live: dword (t, r) of an operand with R rows
+// per step is at byte off + 4 (t R + r) of the workspace.
+struct ScaleSrc {
+  uint32_t off;     // byte offset of the operand's [step][row] array in the workspace
+  uint32_t rows;    // R: rows per step of that array
+  uint32_t row0;    // first row of the tile
 };
-
-template <class C>
-__device__ __forceinline__ void make_plan(LoadPlan<C>& P, const Operand& X, const Operand& W) {
-  const int wave = wave_id();
-  const int lane = threadIdx.x % kWave;
-#pragma unroll
-  for (int i = 0; i < C::QX; ++i) {
-    int q = wave * C::QX + i;
-    int row = q * 8 + lane / 8;
-    int c = (lane & 7) ^ swz8(row);
-    P.xoff[i] = (uint32_t)row * X.ld + (uint32_t)c * 16u;
-    P.xk[i] = c * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < C::QW; ++i) {
-    int q = wave * C::QW + i;
-    if constexpr (C::WFMT == MXGG_FMT_E2M1) {
-      int row = q * 16 + lane / 4;
-      int c = (lane & 3) ^ swz4(row);
-      P.woff[i] = (uint32_t)row * W.ld + (uint32_t)c * 16u;
-      P.wk[i] = c * 32;
-    } else {
-      int row = q * 8 + lane / 8;
-      int c = (lane & 7) ^ swz8(row);
-      P.woff[i] = (uint32_t)row * W.ld + (uint32_t)c * 16u;
-      P.wk[i] = c * 16;
-    }
-  }
-  const int wm = wave / C::WGN, wn = wave % C::WGN;
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i) P.xs_off[i] = (uint32_t)(wm * C::WTM + i * 32 + lane % 32) * X.lds;
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j) P.ws_off[j] = (uint32_t)(wn * C::WTN + j * 32 + lane % 32) * W.lds;
-#pragma unroll
-  for (int i = 0; i < C::QS; ++i) {
-    int row = (wave * C::QS + i) * 64 + lane;     // scale rows: X rows then W rows
-    P.s_off[i] = row < C::BM ? (uint32_t)row * X.lds : (uint32_t)(row - C::BM) * W.lds;
-  }
-}
-
-// LDS path: the step's scale dword of every X and W row of the tile, one row
-// per lane, copied global -> LDS next to the data tiles.
-template <class C>
-__device__ __forceinline__ void issue_scales(uint8_t* sb, const Operand& X, const Operand& W,
-                                             const LoadPlan<C>& P, int st) {
-  const int wave = wave_id();
-#pragma unroll
-  for (int i = 0; i < C::QS; ++i) {
-    const int q = wave * C::QS + i;               // 64-row group; uniform per wave
-    const bool isx = q * 64 < C::BM;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(isx ? X.scale : W.scale,
-                                             (lds_ptr_t)(sb + C::XSOFF + q * 256), 4, P.s_off[i],
-                                             (uint32_t)st * 4u, 0, 0);
-  }
-}
-
-// Issue the global->LDS copies of reduction step `st` into stage buffer `sb`.
-// MASKED: chunks whose reduction range falls outside [lo, hi) load zeros.
-template <class C, bool MASKED>
-__device__ __forceinline__ void issue_tiles(uint8_t* sb, const Operand& X, const Operand& W,
-                                            const LoadPlan<C>& P, int st, int lo, int hi) {
-  const int wave = wave_id();
-  const uint32_t xso = (uint32_t)st * C::XROW;
-  const uint32_t wso = (uint32_t)st * C::WROW;
-#pragma unroll
-  for (int i = 0; i < C::QX; ++i) {
-    uint32_t off = P.xoff[i];
-    if constexpr (MASKED) {
-      int k = st * BK + P.xk[i];
-      if (k < lo || k + 16 > hi) off = kOOB;
-    }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(X.data, (lds_ptr_t)(sb + (wave * C::QX + i) * 1024), 16,
-                                             off, xso, 0, 0);
-  }
-  uint8_t* wb = sb + C::XBYTES;
-#pragma unroll
-  for (int i = 0; i < C::QW; ++i) {
-    uint32_t off = P.woff[i];
-    if constexpr (MASKED) {
-      int k = st * BK + P.wk[i];
-      int w = C::WFMT == MXGG_FMT_E2M1 ? 32 : 16;
-      if (k < lo || k + w > hi) off = kOOB;
-    }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(W.data, (lds_ptr_t)(wb + (wave * C::QW + i) * 1024), 16,
-                                             off, wso, 0, 0);
-  }
-}
-
-// Branch-free variant used by the pipelined loop: every load is range-checked
-// with a select, so a step outside [lo, hi) (e.g. a prefetch past the last
-// step) only writes zeros into the stage.
-template <class C>
-__device__ __forceinline__ void issue_tiles_sel(uint8_t* sb, const Operand& X, const Operand& W,
-                                                const LoadPlan<C>& P, int st, int lo, int hi) {
-  const int wave = wave_id();
-  const uint32_t xso = (uint32_t)st * C::XROW;
-  const uint32_t wso = (uint32_t)st * C::WROW;
-  const int kk = st * BK;
-  constexpr int WCH = C::WFMT == MXGG_FMT_E2M1 ? 32 : 16;
-#pragma unroll
-  for (int i = 0; i < C::QX; ++i) {
-    const int k = kk + P.xk[i];
-    const uint32_t off = (k >= lo && k + 16 <= hi) ? P.xoff[i] : kOOB;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(X.data, (lds_ptr_t)(sb + (wave * C::QX + i) * 1024), 16,
-                                             off, xso, 0, 0);
-  }
-  uint8_t* wb = sb + C::XBYTES;
-#pragma unroll
-  for (int i = 0; i < C::QW; ++i) {
-    const int k = kk + P.wk[i];
-    const uint32_t off = (k >= lo && k + WCH <= hi) ? P.woff[i] : kOOB;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(W.data, (lds_ptr_t)(wb + (wave * C::QW + i) * 1024), 16,
-                                             off, wso, 0, 0);
-  }
-}
-
-// Byte mask (0xff per 32-element block) of the step's blocks outside [lo, hi).
-__device__ __forceinline__ uint32_t outside_mask(int st, int lo, int hi) {
-  uint32_t m = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int k = st * BK + 32 * b;
-    m |= (k < lo || k >= hi) ? (0xffu << (8 * b)) : 0u;
-  }
-  return m;
-}
-
-// Scale dwords of step `st`: byte b = scale of the 32-element block 4*st + b.
-template <bool DW>
-__device__ __forceinline__ uint32_t load_scale4(__amdgpu_buffer_rsrc_t r, uint32_t off, int st) {
-  if constexpr (DW) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, (uint32_t)st * 4u, 0);
-  } else {
-    uint32_t v = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      v |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, off + b, (uint32_t)st * 4u, 0) << (8 * b);
-    return v;
-  }
-}
-
-// Replace the scale bytes of 32-element blocks outside [lo, hi) by 127 (2**0)
-// so that masked (zero) data never meets a NaN scale byte.
-__device__ __forceinline__ uint32_t neutralize(uint32_t v, int st, int lo, int hi) {
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    int k = st * BK + 32 * b;
-    if (k < lo || k >= hi) v = (v & ~(0xffu << (8 * b))) | (127u << (8 * b));
-  }
-  return v;
-}
-
-template <class C, bool DW>
-__device__ __forceinline__ void load_scales(uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN],
-                                            const Operand& X, const Operand& W,
-                                            const LoadPlan<C>& P, int st) {
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i) xs[i] = load_scale4<DW>(X.scale, P.xs_off[i], st);
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j) ws[j] = load_scale4<DW>(W.scale, P.ws_off[j], st);
-}
-
-// One 64-element half of a step: fragments from LDS, FM x FN scaled MFMAs.
-template <class C, int H>
-__device__ __forceinline__ void mma_half(const uint8_t* sb, const uint32_t (&xs)[C::FM],
-                                         const uint32_t (&ws)[C::FN],
-                                         v16f (&acc)[C::FM][C::FN]) {
-  const int wave = wave_id();
-  const int lane = threadIdx.x % kWave;
-  const int wm = wave / C::WGN, wn = wave % C::WGN;
-  const int hsel = lane >> 5;
-  const int r32 = lane & 31;
-  const int sw8 = swz8(r32);
-  // X fragment: 16 bytes at k = 64H + 16*hsel and 16 at k = 64H + 32 + 16*hsel
-  const int c0 = (4 * H + hsel) ^ sw8;
-  const int c1 = (4 * H + 2 + hsel) ^ sw8;
-  v8i b[C::FM];
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i) {
-    const uint8_t* row = sb + (wm * C::WTM + i * 32 + r32) * C::XROW;
-    v4i lo = *reinterpret_cast<const v4i*>(row + c0 * 16);
-    v4i hi = *reinterpret_cast<const v4i*>(row + c1 * 16);
-    b[i] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  }
-  v8i a[C::FN];
-  const uint8_t* wb = sb + C::XBYTES;
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j) {
-    const uint8_t* row = wb + (wn * C::WTN + j * 32 + r32) * C::WROW;
-    if constexpr (C::WFMT == MXGG_FMT_E2M1) {
-      // 32 packed fp4 values: k = 64H + 32*hsel .. +31 -> one 16-byte chunk
-      const int c = (2 * H + hsel) ^ swz4(r32);
-      v4i lo = *reinterpret_cast<const v4i*>(row + c * 16);
-      a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
-    } else {
-      v4i lo = *reinterpret_cast<const v4i*>(row + c0 * 16);
-      v4i hi = *reinterpret_cast<const v4i*>(row + c1 * 16);
-      a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-          a[j], b[i], acc[i][j], C::WFMT, MXGG_FMT_E4M3, 2 * H, (int)ws[j], 2 * H, (int)xs[i]);
-    }
-  }
-}
-
-#define MXGG_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
-#define MXGG_BARRIER() asm volatile("s_barrier" ::: "memory")
-// All of this wave's LDS reads have returned, then barrier: the stage may be
-// overwritten by any wave afterwards.
-#define MXGG_RELEASE() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
-// Padding that lets in-flight v_mfma_scale instructions read their operands
-// before the registers can be rewritten: the compiler does not model the
-// scale operands as in-flight reads.
-#define MXGG_MFMA_DRAIN() asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory")
-
-// Reduction over steps [s0, s1) (global 128-element steps) restricted to the
-// element range [lo, hi).  Steps that are not fully inside [lo, hi) are masked.
-// Two LDS stages.  DW (4-byte aligned scale rows): scales travel through LDS
-// with the tiles, so the only vector-memory loads in flight are LDS copies and
-// one explicit vmcnt wait per step orders them.  !DW: scales are gathered
-// byte-wise into registers one step ahead.
-template <class C, bool DW>
-__device__ __forceinline__ void mainloop(uint8_t* smem, const Operand& X, const Operand& W,
-                                         int s0, int s1, int lo, int hi,
-                                         v16f (&acc)[C::FM][C::FN]) {
-  if (s0 >= s1) return;
-  constexpr int NLOAD = C::QX + C::QW + (DW ? C::QS : 0);
-  LoadPlan<C> P;
-  make_plan<C>(P, X, W);
-  const int wave = wave_id();
-  const int lane = threadIdx.x % kWave;
-  const int wm = wave / C::WGN, wn = wave % C::WGN;
-  const int sh = 8 * (lane >> 5);
-  uint32_t xc[C::FM], wc[C::FN], xn[C::FM], wn_[C::FN];
-  auto full = [&](int st) { return st * BK >= lo && st * BK + BK <= hi; };
-
-  if (full(s0)) issue_tiles<C, false>(smem, X, W, P, s0, lo, hi);
-  else issue_tiles<C, true>(smem, X, W, P, s0, lo, hi);
-  if constexpr (DW) issue_scales<C>(smem, X, W, P, s0);
-  else load_scales<C, false>(xc, wc, X, W, P, s0);
-
-  for (int st = s0; st < s1; ++st) {
-    const int cur = (st - s0) & 1;
-    if (st + 1 < s1) {
-      uint8_t* nb = smem + (cur ^ 1) * C::STAGE;
-      if (full(st + 1)) issue_tiles<C, false>(nb, X, W, P, st + 1, lo, hi);
-      else issue_tiles<C, true>(nb, X, W, P, st + 1, lo, hi);
-      if constexpr (DW) issue_scales<C>(nb, X, W, P, st + 1);
-      else load_scales<C, false>(xn, wn_, X, W, P, st + 1);
-      MXGG_WAIT_VM(NLOAD);
-    } else {
-      MXGG_WAIT_VM(0);
-    }
-    MXGG_BARRIER();
-    const uint8_t* sb = smem + cur * C::STAGE;
-    if constexpr (DW) {
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i)
-        xc[i] = *reinterpret_cast<const uint32_t*>(sb + C::XSOFF + (wm * C::WTM + i * 32 + (lane & 31)) * 4);
-#pragma unroll
-      for (int j = 0; j < C::FN; ++j)
-        wc[j] = *reinterpret_cast<const uint32_t*>(sb + C::WSOFF + (wn * C::WTN + j * 32 + (lane & 31)) * 4);
-    }
-    const bool part = !full(st);
-    uint32_t xsh[C::FM], wsh[C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      uint32_t v = xc[i];
-      if (part) v = neutralize(v, st, lo, hi);
-      xsh[i] = v >> sh;
-    }
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      uint32_t v = wc[j];
-      if (part) v = neutralize(v, st, lo, hi);
-      wsh[j] = v >> sh;
-    }
-    mma_half<C, 0>(sb, xsh, wsh, acc);
-    mma_half<C, 1>(sb, xsh, wsh, acc);
-    MXGG_RELEASE();
-    MXGG_MFMA_DRAIN();
-    if constexpr (!DW) {
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i) xc[i] = xn[i];
-#pragma unroll
-      for (int j = 0; j < C::FN; ++j) wc[j] = wn_[j];
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Software-pipelined main loop (aligned-scale path).
-//
-// Per 128-element step s (stage s%2 holds step s, step s+1 is in flight):
-//   half 0: multiply fragments Fa (k 0..63) while the k 64..127 fragments of
-//           the same step are read into Fb;
-//   half 1: issue two MFMAs on Fb, then -- while they run -- wait for step
-//           s+1 to land, take the workgroup barrier (the one barrier of the
-//           step), read step s+1's scales and k 0..63 fragments into Fa,
-//           start the global->LDS copies of step s+2 into the stage just
-//           released, and issue the remaining MFMAs on Fb.
-// Every wave has finished reading stage s%2 (lgkmcnt(0)) before that barrier,
-// so after it the stage can be refilled.
-// ---------------------------------------------------------------------------
 
 template <class C>
 struct Frags {
@@ -399,16 +106,134 @@ struct Frags {
   v8i b[C::FM];   // X fragments (MFMA B operand)
 };
 
-template <class C, int H>
-__device__ __forceinline__ void read_frags(const uint8_t* sb, Frags<C>& F) {
+// Per-lane copy plan.  Data copy i of a wave covers rows q*R .. q*R+R-1
+// (q = wave*Q + i; R = 16 rows of 64 bytes, or 32 rows of 32 bytes for packed
+// e2m1 W); the lane's row inside a copy and its swizzled chunk do not depend
+// on i, so one per-lane offset serves all copies and the row step of copy i
+// travels in the scalar offset.  The chunk index rides in bits 28..31
+// (offsets stay below 2**26: row strides below 2**23).
+// Scale copy of wave w (w < NSD): slot dwords 256 w .. 256 w + 255, 4 per
+// lane; lane l covers step u and tile row v of the group, at workspace byte
+// s_base + t * s_step for step t of the reduction.
+template <class C>
+struct Plan {
+  uint32_t xoff;
+  uint32_t woff;
+  uint32_t s_base;
+  uint32_t s_step;
+};
+
+template <class C>
+__device__ __forceinline__ void make_plan(Plan<C>& P, const Operand& X, const Operand& W,
+                                          const ScaleSrc& xs, const ScaleSrc& ws) {
+  const int lane = threadIdx.x % kWave;
+  {
+    const int row = lane / 4;
+    const int c = (lane & 3) ^ swz4(row);
+    P.xoff = ((uint32_t)row * X.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
+  }
+  if constexpr (C::F4) {
+    const int row = lane / 2;
+    const int c = (lane & 1) ^ swz2(row);
+    P.woff = ((uint32_t)row * W.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
+  } else {
+    const int row = lane / 4;
+    const int c = (lane & 3) ^ swz4(row);
+    P.woff = ((uint32_t)row * W.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
+  }
+  const int q = wave_id() * 256 + 4 * lane;       // first slot dword of the lane
+  const int u = q / (C::BM + C::BN);              // step of the group
+  const int v = q % (C::BM + C::BN);              // tile row: X rows, then W rows
+  const bool isx = v < C::BM;
+  const ScaleSrc& S = isx ? xs : ws;
+  const uint32_t r = S.row0 + (uint32_t)(isx ? v : v - C::BM);
+  P.s_step = S.rows * 4u;
+  P.s_base = S.off + r * 4u + (uint32_t)u * P.s_step;
+}
+
+// Global -> LDS copies of stage `st` (elements [64 st, 64 st + 64)) into slot
+// `sb`.  A 16-byte chunk (16 elements, or 32 packed e2m1) is loaded iff it
+// lies inside [lo, hi); others -- and every chunk of a stage wholly outside,
+// e.g. a prefetch past the last stage -- read as zeros without touching memory.
+template <class C>
+__device__ __forceinline__ void issue_stage(uint8_t* sb, const Operand& X, const Operand& W,
+                                            const Plan<C>& P, int st, int lo, int hi) {
+  const int wave = wave_id();
+  const int kk = st * BKS;
+  constexpr int WE = C::F4 ? 32 : 16;              // elements per W chunk
+  constexpr int WR = C::F4 ? 32 : 16;              // W rows per copy
+  const int xlo = lo - kk <= 0 ? 0 : (lo - kk + 15) / 16;
+  const int xhi = hi - kk <= 0 ? 0 : (hi - kk) / 16;
+  const int wlo = lo - kk <= 0 ? 0 : (lo - kk + WE - 1) / WE;
+  const int whi = hi - kk <= 0 ? 0 : (hi - kk) / WE;
+  const int xc = (int)(P.xoff >> 28), wc = (int)(P.woff >> 28);
+  const uint32_t xo = (xc >= xlo && xc < xhi) ? (P.xoff & 0x0fffffffu) : kOOB;
+  const uint32_t wo = (wc >= wlo && wc < whi) ? (P.woff & 0x0fffffffu) : kOOB;
+#pragma unroll
+  for (int i = 0; i < C::QX; ++i) {
+    const int q = wave * C::QX + i;
+    const uint32_t so = (uint32_t)st * C::XROW + (uint32_t)(q * 16) * X.ld;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(X.data, (lds_ptr_t)(sb + q * 1024), 16, xo, so, 0, 0);
+  }
+  uint8_t* wb = sb + C::XBYTES;
+#pragma unroll
+  for (int i = 0; i < C::QW; ++i) {
+    const int q = wave * C::QW + i;
+    const uint32_t so = (uint32_t)st * C::WROW + (uint32_t)(q * WR) * W.ld;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(W.data, (lds_ptr_t)(wb + q * 1024), 16, wo, so, 0, 0);
+  }
+}
+
+// 16 bytes per lane global -> LDS at LDS byte address `lds` when `go` != 0.
+// The branch lives inside the asm statement, so the loop body stays a single
+// basic block for the compiler (a branch there costs the register allocator
+// dearly); M0 is saved and restored around the copy.  The copy is not known to
+// the compiler: callers order it with explicit vmcnt waits.
+__device__ __forceinline__ void dma16_if(int go, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t saved;
+  asm volatile(
+      "s_cmp_eq_u32 %1, 0\n\t"
+      "s_cbranch_scc1 1f\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %4, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0\n"
+      "1:"
+      : "=&s"(saved)
+      : "s"(go), "v"(voff), "s"(lds), "s"(rsrc)
+      : "memory", "scc");
+#endif
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)(const_cast<void*>(p));
+}
+
+// Scale group g (steps tg .. tg+SCG-1) into scale slot `ss` (waves w < NSD
+// copy 1 KB each).
+template <class C>
+__device__ __forceinline__ void issue_scales(uint8_t* ss, __amdgpu_buffer_rsrc_t wsr, const Plan<C>& P,
+                                             int tg, bool live) {
+  const int wave = wave_id();
+  const int go = (live && wave < C::NSD) ? 1 : 0;
+  dma16_if(uniform(go), wsr, P.s_base + (uint32_t)tg * P.s_step, lds_addr(ss + wave * 1024));
+}
+
+// Fragments and raw scale dwords of the stage in data slot `sb`, whose step is
+// step u of the group held in scale slot `ss`.
+template <class C>
+__device__ __forceinline__ void read_stage(const uint8_t* sb, const uint8_t* ss, int u, Frags<C>& F,
+                                           uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN]) {
   const int wave = wave_id();
   const int lane = threadIdx.x % kWave;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
   const int hsel = lane >> 5;
   const int r32 = lane & 31;
-  const int sw8 = swz8(r32);
-  const int c0 = (4 * H + hsel) ^ sw8;
-  const int c1 = (4 * H + 2 + hsel) ^ sw8;
+  const int sw = swz4(r32);
+  const int c0 = hsel ^ sw;            // elements 16 hsel .. +15
+  const int c1 = (2 + hsel) ^ sw;      // elements 32 + 16 hsel .. +15
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) {
     const uint8_t* row = sb + (wm * C::WTM + i * 32 + r32) * C::XROW;
@@ -420,9 +245,9 @@ __device__ __forceinline__ void read_frags(const uint8_t* sb, Frags<C>& F) {
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) {
     const uint8_t* row = wb + (wn * C::WTN + j * 32 + r32) * C::WROW;
-    if constexpr (C::WFMT == MXGG_FMT_E2M1) {
-      const int c = (2 * H + hsel) ^ swz4(r32);
-      v4i lo = *reinterpret_cast<const v4i*>(row + c * 16);
+    if constexpr (C::F4) {
+      // 32 packed fp4 values, elements 32 hsel .. +31: one 16-byte chunk
+      v4i lo = *reinterpret_cast<const v4i*>(row + (hsel ^ swz2(r32)) * 16);
       F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], 0, 0, 0, 0};
     } else {
       v4i lo = *reinterpret_cast<const v4i*>(row + c0 * 16);
@@ -430,54 +255,39 @@ __device__ __forceinline__ void read_frags(const uint8_t* sb, Frags<C>& F) {
       F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
+  const uint32_t* sx = reinterpret_cast<const uint32_t*>(ss) + u * (C::BM + C::BN);
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) xs[i] = sx[wm * C::WTM + i * 32 + r32];
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) ws[j] = sx[C::BM + wn * C::WTN + j * 32 + r32];
 }
 
-// Scale dwords of the step in stage `sb`, shifted so that op_sel 2*H picks
-// the byte of the lane's 32-element block; blocks outside [lo, hi) neutral.
+// Move the scale byte of the lane's 32-element block of stage st (block
+// 2 st + hsel: byte 2 (st & 1) + hsel of the step's dword) to byte 0, where
+// op_sel 0 reads it; blocks outside [lo, hi) get the neutral scale 127, so
+// zero-filled data never meets a NaN scale byte.
 template <class C>
-__device__ __forceinline__ void read_scales_raw(const uint8_t* sb, uint32_t (&xs)[C::FM],
-                                                uint32_t (&ws)[C::FN]) {
-  const int wave = wave_id();
-  const int lane = threadIdx.x % kWave;
-  const int wm = wave / C::WGN, wn = wave % C::WGN;
+__device__ __forceinline__ void finish_scales(uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN], int st, int lo,
+                                              int hi) {
+  const int hsel = (threadIdx.x % kWave) >> 5;
+  const int sh = 8 * hsel + 16 * (st & 1);
+  const int k = st * BKS + 32 * hsel;
+  const bool out = k < lo || k >= hi;
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-    xs[i] = *reinterpret_cast<const uint32_t*>(sb + C::XSOFF + (wm * C::WTM + i * 32 + (lane & 31)) * 4);
+  for (int i = 0; i < C::FM; ++i) xs[i] = out ? 127u : (xs[i] >> sh);
 #pragma unroll
-  for (int j = 0; j < C::FN; ++j)
-    ws[j] = *reinterpret_cast<const uint32_t*>(sb + C::WSOFF + (wn * C::WTN + j * 32 + (lane & 31)) * 4);
+  for (int j = 0; j < C::FN; ++j) ws[j] = out ? 127u : (ws[j] >> sh);
 }
 
-// Neutralize the blocks of step st outside [lo, hi) and shift so that op_sel
-// 2*H picks the byte of the lane's 32-element block.
-template <class C>
-__device__ __forceinline__ void finish_scales(uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN], int st,
-                                              int lo, int hi) {
-  const int sh = 8 * ((threadIdx.x % kWave) >> 5);
-  const uint32_t m = outside_mask(st, lo, hi);        // wave-uniform
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i) xs[i] = ((xs[i] & ~m) | (0x7f7f7f7fu & m)) >> sh;
-#pragma unroll
-  for (int j = 0; j < C::FN; ++j) ws[j] = ((ws[j] & ~m) | (0x7f7f7f7fu & m)) >> sh;
-}
-
-// MFMAs number [B, E) of the half's FM x FN grid (row-major over (i, j)).
-template <class C, int H, int B, int E>
+template <class C, int B, int E>
 __device__ __forceinline__ void mfma_range(const Frags<C>& F, const uint32_t (&xs)[C::FM],
                                            const uint32_t (&ws)[C::FN], v16f (&acc)[C::FM][C::FN]) {
 #pragma unroll
   for (int t = B; t < E; ++t) {
     const int i = t / C::FN, j = t % C::FN;
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-        F.a[j], F.b[i], acc[i][j], C::WFMT, MXGG_FMT_E4M3, 2 * H, (int)ws[j], 2 * H, (int)xs[i]);
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.a[j], F.b[i], acc[i][j], C::WFMT,
+                                                                 MXGG_FMT_E4M3, 0, (int)ws[j], 0, (int)xs[i]);
   }
-}
-
-template <class C>
-__device__ __forceinline__ void issue_step(uint8_t* sb, const Operand& X, const Operand& W,
-                                           const LoadPlan<C>& P, int st, int lo, int hi) {
-  issue_tiles_sel<C>(sb, X, W, P, st, lo, hi);
-  issue_scales<C>(sb, X, W, P, st);
 }
 
 // Keep the MFMA operand registers of a region allocated until the region's
@@ -494,123 +304,106 @@ __device__ __forceinline__ void hold(const FR& F, const uint32_t (&xs)[NM], cons
 #endif
 }
 
+#define MXGG_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+#define MXGG_BARRIER() asm volatile("s_barrier" ::: "memory")
 #define MXGG_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// Scheduling recipe for one region: NM MFMAs with NV VMEM reads and ND DS
-// reads spread evenly between them (sched_group_barrier groups, in order).
-template <int I, int NM, int NV, int ND>
+// Scheduling recipe: NM MFMAs with the ND DS reads spread over the first NMD
+// of them and the NV VMEM issues (LDS-DMA copies) over the rest, so every read
+// is issued before any copy.
+template <int I, int NM, int NMD, int ND, int NV>
 __device__ __forceinline__ void interleave_step() {
   if constexpr (I < NM) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // 1 MFMA
-    constexpr int v = (NV * (I + 1)) / NM - (NV * I) / NM;
-    constexpr int d = (ND * (I + 1)) / NM - (ND * I) / NM;
-    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);   // VMEM (incl. LDS DMA)
-    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);   // DS reads
-    interleave_step<I + 1, NM, NV, ND>();
+    if constexpr (I < NMD) {
+      constexpr int d = (ND * (I + 1)) / NMD - (ND * I) / NMD;
+      if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);   // DS reads
+    } else {
+      constexpr int J = I - NMD, NR = NM - NMD;
+      constexpr int v = (NV * (J + 1)) / NR - (NV * J) / NR;
+      if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);   // VMEM
+    }
+    interleave_step<I + 1, NM, NMD, ND, NV>();
   }
 }
 
-template <int NM, int NV, int ND>
-__device__ __forceinline__ void interleave() {
-  interleave_step<0, NM, NV, ND>();
-}
-
-// One steady-state step st (a next step exists).  Scales of step st are in
-// (xs, ws); step st+1's are produced into (xn, wn).  The step ends with a drain
-// so that the caller may then overwrite (xs, ws).
+// One stage: multiply stage s0 + r (Fc, xc, wc), read stage s0 + r + 1 into
+// (Fn, xn, wn), start the copies of stage s0 + r + NS and, when stage
+// s0 + r + 1 opens a scale group, the scales of the group after it.
+// (s0 is the ring's first stage, even, in slot 0; t0 = s0 / 2 its step.)
 template <class C>
-__device__ __forceinline__ void pipe_step(uint8_t* smem, const Operand& X, const Operand& W,
-                                          const LoadPlan<C>& P, int s0, int st, int lo, int hi,
-                                          Frags<C>& Fa, Frags<C>& Fb, uint32_t (&xs)[C::FM],
-                                          uint32_t (&ws)[C::FN], uint32_t (&xn)[C::FM],
-                                          uint32_t (&wn)[C::FN], v16f (&acc)[C::FM][C::FN]) {
+__device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, const Operand& W,
+                                           __amdgpu_buffer_rsrc_t wsr, const Plan<C>& P, int s0, int r,
+                                           int lo, int hi, Frags<C>& Fc, uint32_t (&xc)[C::FM],
+                                           uint32_t (&wc)[C::FN], Frags<C>& Fn, uint32_t (&xn)[C::FM],
+                                           uint32_t (&wn)[C::FN], v16f (&acc)[C::FM][C::FN]) {
   constexpr int NMMA = C::FM * C::FN;
-  constexpr int NEARLY = NMMA >= 8 ? 2 : 1;    // MFMAs of half 1 issued before the barrier
-  constexpr int NDS0 = C::FM * 2 + (C::WFMT == MXGG_FMT_E2M1 ? C::FN : C::FN * 2);
-  const int cur = (st - s0) & 1;
-  uint8_t* sb = smem + cur * C::STAGE;
-  uint8_t* nb = smem + (cur ^ 1) * C::STAGE;
-  // ---- half 0: MFMAs on Fa, reads of the second half into Fb in between
-  read_frags<C, 1>(sb, Fb);
-  mfma_range<C, 0, 0, NMMA>(Fa, xs, ws, acc);
-  interleave<NMMA, 0, NDS0>();
+  constexpr int NE = NMMA >= 8 ? 2 : 1;       // MFMAs issued ahead of the barrier
+  constexpr int NDS = C::FM * 2 + (C::F4 ? C::FN : C::FN * 2) + C::FM + C::FN;
+  const int rn = r + 1;
+  uint8_t* cur = smem + (r % C::NS) * C::STAGE;
+  const uint8_t* nxt = smem + (rn % C::NS) * C::STAGE;
+  const uint8_t* snx = smem + C::SOFF + ((rn / SPG) & 1) * C::SSLOT;
+  mfma_range<C, 0, NE>(Fc, xc, wc, acc);
   MXGG_SCHED_FENCE();
-  hold(Fa, xs, ws);
-  // ---- half 1
+  MXGG_WAIT_VM((C::NS - 2) * C::LPS);       // this wave's copies of stage r+1 have landed
+  MXGG_BARRIER();                           // ... every wave's; and stage r's slot is free
+  MXGG_SCHED_FENCE();
+  // LDS reads first, then the copies: a read issued after an LDS-DMA load
+  // may otherwise be given the load's offset register as its destination
+  // while the load still uses it.
+  read_stage<C>(nxt, snx, (rn / 2) % SCG, Fn, xn, wn);
+  // stage r+1 opening scale group g = (r+1)/SPG frees the slot of group g-1
+  // (last read, of stage r, before this barrier): group g+1 goes there
+  const bool opens = rn % SPG == 0;
+  issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, wsr, P, s0 / 2 + (rn / SPG + 1) * SCG,
+                  opens);
+  issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
+  mfma_range<C, NE, NMMA>(Fc, xc, wc, acc);
+  interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, C::LPS>();
+  MXGG_SCHED_FENCE();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  mfma_range<C, 1, 0, NEARLY>(Fb, xs, ws, acc);
-  MXGG_SCHED_FENCE();
-  MXGG_WAIT_VM(0);
-  MXGG_BARRIER();
-  MXGG_SCHED_FENCE();
-  // step st+1's scales and first-half fragments are read before the copies of
-  // step st+2 are issued into the stage just released (past the end: zeros,
-  // never read).  Reads issued in between those LDS-DMA loads came back
-  // corrupted when the compiler gave a read a destination register that a
-  // just-issued DMA load used as its offset.
-  read_scales_raw<C>(nb, xn, wn);
-  read_frags<C, 0>(nb, Fa);
-  issue_step<C>(sb, X, W, P, st + 2, lo, hi);
-  mfma_range<C, 1, NEARLY, NMMA>(Fb, xs, ws, acc);
-  MXGG_SCHED_FENCE();
-  hold(Fb, xs, ws);
-  MXGG_MFMA_DRAIN();
-  MXGG_SCHED_FENCE();
-  finish_scales<C>(xn, wn, st + 1, lo, hi);
-}
-
-template <class C>
-__device__ __forceinline__ void pipe_last(const uint8_t* sb, Frags<C>& Fa, Frags<C>& Fb,
-                                          const uint32_t (&xs)[C::FM], const uint32_t (&ws)[C::FN],
-                                          v16f (&acc)[C::FM][C::FN]) {
-  constexpr int NMMA = C::FM * C::FN;
-  read_frags<C, 1>(sb, Fb);
-  mfma_range<C, 0, 0, NMMA>(Fa, xs, ws, acc);
-  mfma_range<C, 1, 0, NMMA>(Fb, xs, ws, acc);
-  MXGG_SCHED_FENCE();
-  hold(Fa, xs, ws);
-  hold(Fb, xs, ws);
-  MXGG_MFMA_DRAIN();
+  finish_scales<C>(xn, wn, s0 + rn, lo, hi);
+  // keep the current set allocated past the rewrite of the next one
+  hold(Fc, xc, wc);
   MXGG_SCHED_FENCE();
 }
 
+// Reduction over the 64-element stages [s0, s1) restricted to the element
+// range [lo, hi) (chunks and scale blocks outside it are zero / neutral).
+// The ring starts at the even stage s0 & ~1 so that scale groups cover whole
+// steps; an odd stage count runs one stage past s1.  Those extra stages are
+// wholly outside [lo, hi): zero data, neutral scales, exactly zero added.
 template <class C>
-__device__ __forceinline__ void mainloop_pipe(uint8_t* smem, const Operand& X, const Operand& W,
-                                              int s0, int s1, int lo, int hi,
+__device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, const Operand& W,
+                                              __amdgpu_buffer_rsrc_t wsr, const ScaleSrc& xss,
+                                              const ScaleSrc& wss, int s0, int s1, int lo, int hi,
                                               v16f (&acc)[C::FM][C::FN]) {
   if (s0 >= s1) return;
-  constexpr int NLOAD = C::QX + C::QW + C::QS;
-  LoadPlan<C> P;
-  make_plan<C>(P, X, W);
-
-  issue_step<C>(smem, X, W, P, s0, lo, hi);
-  if (s0 + 1 < s1) {
-    issue_step<C>(smem + C::STAGE, X, W, P, s0 + 1, lo, hi);
-    MXGG_WAIT_VM(NLOAD);
-  } else {
-    MXGG_WAIT_VM(0);
-  }
+  s0 &= ~1;
+  Plan<C> P;
+  make_plan<C>(P, X, W, xss, wss);
+  // scale groups 0 and 1, then stages s0 .. s0+NS-1 (scales first: every
+  // wait for a stage's copies then covers the scale copies issued before it)
+  issue_scales<C>(smem + C::SOFF, wsr, P, s0 / 2, true);
+  issue_scales<C>(smem + C::SOFF + C::SSLOT, wsr, P, s0 / 2 + SCG, true);
+#pragma unroll
+  for (int i = 0; i < C::NS; ++i) issue_stage<C>(smem + i * C::STAGE, X, W, P, s0 + i, lo, hi);
+  MXGG_WAIT_VM((C::NS - 1) * C::LPS);
   MXGG_BARRIER();
   Frags<C> Fa, Fb;
   uint32_t xa[C::FM], wa[C::FN], xb[C::FM], wb[C::FN];
-  read_scales_raw<C>(smem, xa, wa);
-  read_frags<C, 0>(smem, Fa);
+  read_stage<C>(smem, smem + C::SOFF, 0, Fa, xa, wa);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   finish_scales<C>(xa, wa, s0, lo, hi);
-
-  // steady state: a next step always exists
-  int st = s0;
-  for (; st + 1 < s1; ++st) {
-    pipe_step<C>(smem, X, W, P, s0, st, lo, hi, Fa, Fb, xa, wa, xb, wb, acc);
-    // xb/wb now hold step st+1's scales; move them into the current set only
-    // after the step's last MFMAs have read xa/wa (pipe_step ends with a drain)
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) xa[i] = xb[i];
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) wa[j] = wb[j];
+  const int n = s1 - s0;
+#pragma nounroll
+  for (int r = 0; r < n; r += 2) {
+    ring_stage<C>(smem, X, W, wsr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+    ring_stage<C>(smem, X, W, wsr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
   }
-  pipe_last<C>(smem + ((st - s0) & 1) * C::STAGE, Fa, Fb, xa, wa, acc);
-  // the zero-filled prefetch past the last step may still be writing LDS:
-  // drain it before the workgroup can exit and its LDS be reallocated
+  // copies past the last stage (zero fills, scale groups) may still be
+  // writing LDS: drain them before the LDS is reused or released
   MXGG_WAIT_VM(0);
 }
 
@@ -698,7 +491,7 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], 
                                                int out_dtype) {
   constexpr int RB = C::WTN * 2;                 // staged row bytes
   constexpr int NCH = RB / 16;                   // 16-byte chunks per row
-  constexpr int AVAIL = 2 * C::STAGE / C::NW;    // LDS bytes per wave
+  constexpr int AVAIL = C::LDS / C::NW;           // LDS bytes per wave
   constexpr int FPP = store_pass_rows(C::FM, AVAIL / (32 * RB));   // fragment rows per pass
   static_assert(FPP >= 1 && C::FM % FPP == 0, "store staging");
   static_assert(64 % NCH == 0, "store row width");
@@ -759,20 +552,91 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], 
 }
 
 // ---------------------------------------------------------------------------
+// scale re-layout: plain (rows, nblk) e8m0 scales -> [batch][step][row] dwords
+// ---------------------------------------------------------------------------
+
+// One operand's scales: `batches` blocks of `rows` rows (row r of batch b at
+// src + b * ld_b + r * ld_r), nblk = K/32 bytes per row.  Output dword
+// (b, t, r) at dst[(b * steps + t) * rows + r] holds bytes 4t .. 4t+3 of the
+// row; bytes past nblk are 127 (2**0), so a partial last step needs no
+// masking in the GEMM.
+struct ScaleJob {
+  const uint8_t* src; int64_t ld_r; int64_t ld_b;
+  uint32_t* dst; int rows; int batches; int nblk; int steps;
+  int tiles_r; int tiles_t;      // 64-row x 16-step tiles per batch
+};
+
+struct ScaleJobs {
+  ScaleJob j[2];
+  int tiles0;                    // workgroups of job 0 (job 1 follows)
+};
+
+// 64 rows x 16 steps per workgroup (256 threads): each thread reads 16
+// source bytes of one row (4 steps), the tile is transposed through LDS, and
+// each thread writes 4 dwords of consecutive rows for one step.
+__global__ __launch_bounds__(256) void scale_relayout_kernel(ScaleJobs js) {
+  __shared__ uint32_t tile[16][65];
+  int bid = blockIdx.x;
+  const int which = bid < js.tiles0 ? 0 : 1;
+  const ScaleJob& J = js.j[which];
+  if (which) bid -= js.tiles0;
+  const int per_batch = J.tiles_r * J.tiles_t;
+  const int b = bid / per_batch;
+  const int rt = (bid % per_batch) % J.tiles_r;
+  const int tt = (bid % per_batch) / J.tiles_r;
+  const int r0 = rt * 64, t0 = tt * 16;
+  {
+    const int r = r0 + threadIdx.x / 4;
+    const int tq = threadIdx.x % 4;                // steps t0 + 4 tq .. + 3
+    const uint8_t* row = J.src + (int64_t)b * J.ld_b + (int64_t)r * J.ld_r;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int t = t0 + 4 * tq + s;
+      uint32_t v = 0x7f7f7f7fu;
+      if (r < J.rows) {
+        v = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int blk = 4 * t + q;
+          const uint32_t byte = blk < J.nblk ? (uint32_t)row[blk] : 127u;
+          v |= byte << (8 * q);
+        }
+      }
+      tile[4 * tq + s][threadIdx.x / 4] = v;
+    }
+  }
+  __syncthreads();
+  {
+    const int ts = threadIdx.x / 16;               // step of the tile
+    const int rq = threadIdx.x % 16;               // rows 4 rq .. 4 rq + 3
+    const int t = t0 + ts;
+    if (t < J.steps) {
+      uint32_t* out = J.dst + ((int64_t)b * J.steps + t) * J.rows;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = r0 + 4 * rq + q;
+        if (r < J.rows) out[r] = tile[ts][4 * rq + q];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // forward / dgrad
 // ---------------------------------------------------------------------------
 
 struct FwdParams {
-  const uint8_t* a; int64_t lda; const uint8_t* as; int64_t ldas;
-  const uint8_t* b; int64_t ldb_n; int64_t ldb_e; const uint8_t* bs; int64_t ldbs_n; int64_t ldbs_e;
+  const uint8_t* a; int64_t lda;
+  const uint8_t* b; int64_t ldb_n; int64_t ldb_e;
+  const uint8_t* ws; uint32_t ws_bytes;     // re-laid scales: A [T][M], then B [E][T][N]
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype; int64_t ldo;
   int grid_n; int group_m; int xcd;
 };
 
-template <class C, bool DW>
+template <class C>
 __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   const int pid = blockIdx.x;
   const int total_m = route_total(p.offs, p.E, C::BM);
   const int tiles = total_m * p.grid_n;
@@ -792,13 +656,13 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
 
   Operand X, W;
   X.ld = (uint32_t)p.lda;
-  X.lds = (uint32_t)p.ldas;
   X.data = make_rsrc(p.a + row0 * p.lda, (uint32_t)rows * X.ld);
-  X.scale = make_rsrc(p.as + row0 * p.ldas, (uint32_t)rows * X.lds);
   W.ld = (uint32_t)p.ldb_n;
-  W.lds = (uint32_t)p.ldbs_n;
   W.data = make_rsrc(p.b + (int64_t)r.expert * p.ldb_e + n0 * p.ldb_n, (uint32_t)cols * W.ld);
-  W.scale = make_rsrc(p.bs + (int64_t)r.expert * p.ldbs_e + n0 * p.ldbs_n, (uint32_t)cols * W.lds);
+  const uint32_t T = (uint32_t)((p.K + STEP - 1) / STEP);
+  const ScaleSrc xs{0u, (uint32_t)p.M, (uint32_t)row0};
+  const ScaleSrc ws{4u * T * ((uint32_t)p.M + (uint32_t)r.expert * (uint32_t)p.N), (uint32_t)p.N, (uint32_t)n0};
+  const __amdgpu_buffer_rsrc_t wsr = make_rsrc(p.ws, p.ws_bytes);
 
   v16f acc[C::FM][C::FN];
 #pragma unroll
@@ -807,12 +671,11 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 
   const int K = (int)p.K;
-  if constexpr (DW) mainloop_pipe<C>(smem, X, W, 0, (K + BK - 1) / BK, 0, K, acc);
-  else mainloop<C, DW>(smem, X, W, 0, (K + BK - 1) / BK, 0, K, acc);
+  ring_mainloop<C>(smem, X, W, wsr, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
 
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
-  if (DW && esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
+  if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
     store_tile_lds<C>(acc, smem, o, p.ldo, rows, cols, p.out_dtype);
   else
     store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
@@ -824,16 +687,17 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 
 struct WgradParams {
-  const uint8_t* go; int64_t ld_go; const uint8_t* gos; int64_t ld_gos;
-  const uint8_t* ia; int64_t ld_ia; const uint8_t* ias; int64_t ld_ias;
+  const uint8_t* go; int64_t ld_go;
+  const uint8_t* ia; int64_t ld_ia;
+  const uint8_t* ws; uint32_t ws_bytes;     // re-laid scales: GO [T][N], then IA [T][K]
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype;
   int tiles_n; int tiles_k;
 };
 
-template <class C, bool DW>
+template <class C>
 __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   const int g = blockIdx.y;
   const int tn = blockIdx.x / p.tiles_k;       // X side: rows of go_t (output rows n)
   const int tk = blockIdx.x % p.tiles_k;       // W side: rows of ia_t (output cols k)
@@ -847,13 +711,13 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 
   Operand X, W;
   X.ld = (uint32_t)p.ld_go;
-  X.lds = (uint32_t)p.ld_gos;
   X.data = make_rsrc(p.go + n0 * p.ld_go, (uint32_t)rows * X.ld);
-  X.scale = make_rsrc(p.gos + n0 * p.ld_gos, (uint32_t)rows * X.lds);
   W.ld = (uint32_t)p.ld_ia;
-  W.lds = (uint32_t)p.ld_ias;
   W.data = make_rsrc(p.ia + k0 * p.ld_ia, (uint32_t)cols * W.ld);
-  W.scale = make_rsrc(p.ias + k0 * p.ld_ias, (uint32_t)cols * W.lds);
+  const uint32_t T = (uint32_t)((p.M + STEP - 1) / STEP);
+  const ScaleSrc xs{0u, (uint32_t)p.N, (uint32_t)n0};
+  const ScaleSrc ws{4u * T * (uint32_t)p.N, (uint32_t)p.K, (uint32_t)k0};
+  const __amdgpu_buffer_rsrc_t wsr = make_rsrc(p.ws, p.ws_bytes);
 
   v16f acc[C::FM][C::FN];
 #pragma unroll
@@ -861,14 +725,11 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 
-  if (hi > lo) {
-    if constexpr (DW) mainloop_pipe<C>(smem, X, W, lo / BK, (hi + BK - 1) / BK, lo, hi, acc);
-    else mainloop<C, DW>(smem, X, W, lo / BK, (hi + BK - 1) / BK, lo, hi, acc);
-  }
+  if (hi > lo) ring_mainloop<C>(smem, X, W, wsr, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
 
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
-  if (DW && esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
+  if (esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
     store_tile_lds<C>(acc, smem, o, p.K, rows, cols, p.out_dtype);
   else
     store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
@@ -929,9 +790,9 @@ using namespace mxgg;
 
 namespace {
 
-typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3> CfgF8_256;
-typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3> CfgF8_128;
-typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1> CfgF4_256;
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_256;
+typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_128;
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 5> CfgF4_256;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -952,7 +813,7 @@ FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, in
 }
 
 template <class C>
-int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, bool dw, hipStream_t st) {
+int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, hipStream_t st) {
   FwdParams p = p0;
   p.grid_n = (int)cdiv(p.N, C::BN);
   p.group_m = gm;
@@ -960,9 +821,28 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, bool dw, hip
   const int64_t grid = (int64_t)grid_m_ub * p.grid_n;
   if (grid <= 0) return MXGG_OK;
   if (grid > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
-  if (dw) hipLaunchKernelGGL((fwd_kernel<C, true>), dim3((unsigned)grid), dim3(C::NT), 0, st, p);
-  else hipLaunchKernelGGL((fwd_kernel<C, false>), dim3((unsigned)grid), dim3(C::NT), 0, st, p);
+  hipLaunchKernelGGL((fwd_kernel<C>), dim3((unsigned)grid), dim3(C::NT), 0, st, p);
   return launch_status("grouped_mm");
+}
+
+ScaleJob scale_job(const uint8_t* src, int64_t ld_r, int64_t ld_b, uint32_t* dst, int64_t rows,
+                   int batches, int64_t nblk, int64_t steps) {
+  ScaleJob j{src, ld_r, ld_b, dst, (int)rows, batches, (int)nblk, (int)steps,
+             (int)cdiv(rows, 64), (int)cdiv(steps, 16)};
+  return j;
+}
+
+// Re-lay two operands' scales into the workspace (one launch).
+int launch_relayout(const ScaleJob& a, const ScaleJob& b, hipStream_t st, const char* what) {
+  ScaleJobs js;
+  js.j[0] = a;
+  js.j[1] = b;
+  js.tiles0 = a.batches * a.tiles_r * a.tiles_t;
+  const int64_t grid = (int64_t)js.tiles0 + (int64_t)b.batches * b.tiles_r * b.tiles_t;
+  if (grid <= 0) return MXGG_OK;
+  if (grid > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "%s: scale re-layout grid too large", what);
+  hipLaunchKernelGGL(scale_relayout_kernel, dim3((unsigned)grid), dim3(256), 0, st, js);
+  return launch_status(what);
 }
 
 }  // namespace
@@ -1009,12 +889,17 @@ extern "C" int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t
 
 static bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
+extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
+  if (E <= 0 || M < 0 || N < 0 || K < 0) return 0;
+  return (size_t)4 * (size_t)cdiv(K, STEP) * ((size_t)M + (size_t)E * (size_t)N);
+}
+
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
                                const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
                                const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
                                const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
                                void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
-                               int group_m, int xcd, void* stream) {
+                               int group_m, int xcd, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: weight format %d not E4M3/E2M1", b_fmt);
@@ -1023,8 +908,6 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: E=%d out of range", E);
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: negative shape");
   if (K % 32) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: K=%lld must be a multiple of 32", (long long)K);
-  if (b_fmt == MXGG_FMT_E2M1 && K % 128)
-    return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: e2m1 weights need K %% 128 == 0");
   const int64_t kb = b_fmt == MXGG_FMT_E2M1 ? K / 2 : K;
   if (lda < K || ldas < K / 32 || ldb_n < kb || ldbs_n < K / 32 || ldo < N)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: a row stride is smaller than its row");
@@ -1032,29 +915,39 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: expert stride smaller than one expert");
   if (lda % 16 || ldb_n % 16 || !aligned16(A) || !aligned16(B))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: A/B rows must be 16-byte aligned");
-  if (lda >= (1 << 23) || ldb_n >= (1 << 23) || ldas >= (1 << 23) || ldbs_n >= (1 << 23))
+  if (lda >= (1 << 23) || ldb_n >= (1 << 23))
     return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: row strides must be below 2**23 bytes");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: dimension above 2**31");
   if (M == 0 || N == 0) return MXGG_OK;
   if (!A || !A_s || !B || !B_s || !offs || !out)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: null pointer");
+  const size_t need = mxgg_grouped_mm_workspace_size(E, M, N, K);
+  if (need >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: problem too large");
+  if (need && (!workspace || ws_bytes < need))
+    return fail(MXGG_ERR_WORKSPACE, "grouped_mm: workspace of %zu bytes needed, %zu given", need,
+                workspace ? ws_bytes : (size_t)0);
   if (int rc = require_device()) return rc;
   FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
-  const bool dw = (ldas % 4 == 0) && (ldbs_n % 4 == 0) && (ldbs_e % 4 == 0) &&
-                  ((uintptr_t)A_s % 4 == 0) && ((uintptr_t)B_s % 4 == 0);
-  FwdParams p{A, lda, A_s, ldas, B, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
-              (uint8_t*)out, out_dtype, ldo, 0, 0, 0};
+  const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
+                                           : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
+  if (!built) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built", c.bm, c.bn);
   hipStream_t st = (hipStream_t)stream;
-  if (b_fmt == MXGG_FMT_E2M1) {
-    if (c.bm != 256 || c.bn != 256) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: e2m1 build has 256x256 tiles only");
-    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, dw, st);
+  const int64_t T = cdiv(K, STEP);
+  uint32_t* wsd = (uint32_t*)workspace;
+  if (T > 0) {
+    if (int rc = launch_relayout(scale_job(A_s, ldas, 0, wsd, M, 1, K / 32, T),
+                                 scale_job(B_s, ldbs_n, ldbs_e, wsd + T * M, N, E, K / 32, T), st,
+                                 "grouped_mm"))
+      return rc;
   }
-  if (c.bm == 256 && c.bn == 256)
-    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, dw, st);
-  if (c.bm == 128 && c.bn == 128)
-    return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, dw, st);
-  return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built (256x256, 128x128)", c.bm, c.bn);
+  FwdParams p{A, lda, B, ldb_n, ldb_e, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
+              (uint8_t*)out, out_dtype, ldo, 0, 0, 0};
+  if (b_fmt == MXGG_FMT_E2M1)
+    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, st);
+  if (c.bm == 256)
+    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, st);
+  return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, st);
 }
 
 extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,
@@ -1076,8 +969,9 @@ extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, in
 }
 
 extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
-  (void)E; (void)M; (void)N; (void)K;
-  return 0;
+  (void)E;
+  if (M < 0 || N < 0 || K < 0) return 0;
+  return (size_t)4 * (size_t)cdiv(M, STEP) * ((size_t)N + (size_t)K);
 }
 
 extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
@@ -1085,7 +979,6 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
                           const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
                           int out_dtype, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
-  (void)workspace; (void)ws_bytes;
   if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: out_dtype %d not BF16/F32", out_dtype);
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "wgrad: E=%d out of range", E);
@@ -1095,24 +988,33 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: a row stride is smaller than its row");
   if (ld_go % 16 || ld_ia % 16 || !aligned16(go_t) || !aligned16(ia_t))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: operand rows must be 16-byte aligned");
-  if (ld_go >= (1 << 23) || ld_ia >= (1 << 23) || ld_gos >= (1 << 23) || ld_ias >= (1 << 23))
+  if (ld_go >= (1 << 23) || ld_ia >= (1 << 23))
     return fail(MXGG_ERR_UNSUPPORTED, "wgrad: row strides must be below 2**23 bytes");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MXGG_ERR_UNSUPPORTED, "wgrad: dimension above 2**31");
   if (N == 0 || K == 0) return MXGG_OK;
   if (!go_t || !go_s || !ia_t || !ia_s || !offs || !out)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: null pointer");
+  const size_t need = mxgg_wgrad_workspace_size(E, M, N, K);
+  if (need >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: problem too large");
+  if (need && (!workspace || ws_bytes < need))
+    return fail(MXGG_ERR_WORKSPACE, "wgrad: workspace of %zu bytes needed, %zu given", need,
+                workspace ? ws_bytes : (size_t)0);
   if (int rc = require_device()) return rc;
   typedef CfgF8_256 C;
-  WgradParams p{go_t, ld_go, go_s, ld_gos, ia_t, ld_ia, ia_s, ld_ias, offs, E, M, N, K,
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t T = cdiv(M, STEP);
+  uint32_t* wsd = (uint32_t*)workspace;
+  if (T > 0) {
+    if (int rc = launch_relayout(scale_job(go_s, ld_gos, 0, wsd, N, 1, M / 32, T),
+                                 scale_job(ia_s, ld_ias, 0, wsd + T * N, K, 1, M / 32, T), st, "wgrad"))
+      return rc;
+  }
+  WgradParams p{go_t, ld_go, ia_t, ld_ia, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
                 (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN)};
-  const bool dw = (ld_gos % 4 == 0) && (ld_ias % 4 == 0) && ((uintptr_t)go_s % 4 == 0) &&
-                  ((uintptr_t)ia_s % 4 == 0);
   const int64_t gx = (int64_t)p.tiles_n * p.tiles_k;
   if (gx > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");
   dim3 grid((unsigned)gx, (unsigned)E);
-  hipStream_t st = (hipStream_t)stream;
-  if (dw) hipLaunchKernelGGL((wgrad_kernel<C, true>), grid, dim3(C::NT), 0, st, p);
-  else hipLaunchKernelGGL((wgrad_kernel<C, false>), grid, dim3(C::NT), 0, st, p);
+  hipLaunchKernelGGL((wgrad_kernel<C>), grid, dim3(C::NT), 0, st, p);
   return launch_status("wgrad");
 }

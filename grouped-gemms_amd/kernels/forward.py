@@ -119,6 +119,9 @@ def triton_mxfp8_grouped_mm(
     out = torch.empty((M, N), dtype=out_dtype, device=dev)
     code = _out_code(out_dtype)
     lib = _lib.load()
+    # scratch for the scales re-laid step-major (overwritten by the call)
+    ws_bytes = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_grouped_mm(
         a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),
         b.data_ptr(), b_fmt, b.stride(1), b.stride(0),
@@ -126,6 +129,7 @@ def triton_mxfp8_grouped_mm(
         offs.data_ptr(), E, M, N, K,
         out.data_ptr(), code, out.stride(0),
         int(bm), int(bn), int(GROUP_M or 0), int(XCD_SWIZZLE or 0),
+        ws.data_ptr() if ws is not None else None, ws_bytes,
         _stream_handle(dev))
     _lib.check(rc)
     return out

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_VERSION 1000 /* major*1000 + minor */
+#define MXGG_VERSION 2000 /* major*1000 + minor */
 
 /* status codes */
 #define MXGG_OK 0
@@ -137,14 +137,22 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            written (as in the reference).
  *   block_m, block_n, group_m, xcd_swizzle: 0 = library choice; otherwise a
  *            request honoured when the build has that tile shape.
- * K must be a multiple of 32 (of 128 for the e2m1 weight format).
+ *   workspace / ws_bytes: device scratch of at least
+ *            mxgg_grouped_mm_workspace_size(E, M, N, K) bytes (4 * ceil(K/128) *
+ *            (M + E*N)): the scales re-laid step-major for the kernel (the
+ *            reference re-lays them per call too, kernels/forward.py:537-550).
+ *            Its contents need not be initialised and are overwritten.
+ * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
+ * rows need no alignment.
  */
+size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
                     const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
                     const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
                     const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
                     void* out, int out_dtype, int64_t ldo,
-                    int block_m, int block_n, int group_m, int xcd_swizzle, void* stream);
+                    int block_m, int block_n, int group_m, int xcd_swizzle,
+                    void* workspace, size_t ws_bytes, void* stream);
 
 /*
  * Weight-gradient grouped GEMM: out[g] = GO[:, s:e] @ IA[:, s:e]^T, shape (E, N, K),
@@ -156,7 +164,8 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
  *   offs  (E,) int32 cumulative group ends, multiples of 32, offs[E-1] <= M
  *   out   (E, N, K) of out_dtype (BF16 or F32), contiguous
  *   workspace / ws_bytes: device scratch of at least
- *         mxgg_wgrad_workspace_size(E, M, N, K) bytes (may be NULL when that is 0)
+ *         mxgg_wgrad_workspace_size(E, M, N, K) bytes (4 * ceil(M/128) * (N + K)):
+ *         the scales re-laid step-major; need not be initialised
  */
 size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,

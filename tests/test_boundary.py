@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.mxgg_version() == 1000
+    assert lib.mxgg_version() == 2000
     assert isinstance(lib.mxgg_last_error_string(), bytes)
 
 
@@ -83,9 +83,24 @@ def test_grouped_mm_validation_without_gpu(args, needle):
     p.update(args)
     rc = lib.mxgg_grouped_mm(p["A"], p["lda"], p["As"], p["ldas"], p["B"], p["b_fmt"], p["ldb_n"],
                              p["ldb_e"], p["Bs"], p["ldbs_n"], p["ldbs_e"], p["offs"], p["E"], p["M"],
-                             p["N"], p["K"], p["out"], p["out_dtype"], p["ldo"], 0, 0, 0, 0, None)
+                             p["N"], p["K"], p["out"], p["out_dtype"], p["ldo"], 0, 0, 0, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID_ARG
     assert needle in lib.mxgg_last_error_string().decode()
+
+
+def test_grouped_mm_workspace_without_gpu():
+    """The scale re-layout scratch is 4 * ceil(K/128) * (M + E*N) bytes; a call
+    without it is rejected (MXGG_ERR_WORKSPACE) before any HIP call."""
+    from kernels import _lib
+    lib = _lib.load()
+    assert lib.mxgg_grouped_mm_workspace_size(8, 16640, 8192, 5120) == 4 * 40 * (16640 + 8 * 8192)
+    assert lib.mxgg_grouped_mm_workspace_size(1, 100, 64, 160) == 4 * 2 * (100 + 64)
+    assert lib.mxgg_wgrad_workspace_size(4, 16640, 2048, 5120) == 4 * 130 * (2048 + 5120)
+    rc = lib.mxgg_grouped_mm(16, 64, 16, 2, 16, 0, 64, 64 * 64, 16, 2, 128, 16, 1, 64, 64, 64,
+                             16, 0, 64, 0, 0, 0, 0, None, 0, None)
+    assert rc == _lib.ERR_WORKSPACE and b"workspace" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_wgrad(16, 64, 16, 2, 16, 64, 16, 2, 16, 1, 64, 8, 8, 16, 0, None, 0, None)
+    assert rc == _lib.ERR_WORKSPACE
 
 
 def test_wgrad_and_quant_validation_without_gpu():
