@@ -65,8 +65,18 @@ def time_call(fn, steps: int, warmup: int, flush_buf):
 
 
 def fwd_kernel_name(cfg: dict) -> str:
-    """Device-kernel name (as rocprofv3 lists it) of a forward/dgrad launch."""
-    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0>, true>"
+    """Device-kernel name (as rocprofv3 lists it) of an e4m3 forward/dgrad launch:
+    Cfg<BLOCK_M, BLOCK_N, waves along M, waves along N, B format, LDS stages>."""
+    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4> >"
+
+
+WGRAD_KERNEL = "mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4> >"
+
+
+def canon(kernel: str) -> str:
+    """Kernel name without return type, arguments and blanks, for matching
+    names across demanglers (``> >`` vs ``>>``)."""
+    return kernel.replace("void ", "").split("(")[0].replace(" ", "")
 
 
 def read_traffic(kernel: str):
@@ -79,7 +89,7 @@ def read_traffic(kernel: str):
     for line in open(path):
         if line.startswith("traffic_bytes_per_launch ") and "=" in line:
             name, val = line[len("traffic_bytes_per_launch "):].rsplit("=", 1)
-            if name.strip() == kernel:
+            if canon(name) == canon(kernel):
                 return float(val)
     return None
 
@@ -158,6 +168,34 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
     return "\n".join(out)
 
 
+def stats_summary(stats_csv: str, bench_json: str) -> str:
+    """Per-kernel table of a ``rocprofv3 --kernel-trace --stats`` run over the
+    default bench (its ``*_kernel_stats.csv``), followed by the same run's own
+    HIP-event figures per GEMM kernel (the JSON line bench.py printed)."""
+    import csv
+    out = [f"{'kernel':78s} {'calls':>6s} {'total ms':>9s} {'avg us':>9s} {'min us':>8s} {'max us':>8s} {'%':>6s}"]
+    for r in csv.DictReader(open(stats_csv)):
+        name = r["Name"].replace("void ", "").split("(")[0]
+        out.append(f"{name[:78]:78s} {int(r['Calls']):6d} {float(r['TotalDurationNs']) / 1e6:9.2f} "
+                   f"{float(r['AverageNs']) / 1e3:9.2f} {float(r['MinNs']) / 1e3:8.1f} "
+                   f"{float(r['MaxNs']) / 1e3:8.1f} {float(r['Percentage']):6.2f}")
+    line = None
+    for text in open(bench_json):
+        if text.startswith("{"):
+            line = json.loads(text)
+    if line and line.get("roofline"):
+        rf = line["roofline"]
+        out += ["", "Same run, bench.py's own figures (HIP events on the launch stream, timed reps only):"]
+        for name, v in sorted(rf["by_kernel"].items()):
+            out.append(f"  {name:58s} avg {v['avg_launch_us']:9.2f} us over {v['launches']:5d} launches, "
+                       f"{v['tflops']:7.1f} TFLOP/s")
+        out.append(f"  dominant kernel {rf['kernel']}: achieved {rf['achieved']} TFLOP/s = {rf['frac']} of "
+                   f"{rf['peak']} (dense MXFP8)")
+        out.append(f"  headline: fwd geomean {line['fwd_geomean_tflops']}  dgrad {line['dgrad_geomean_tflops']}  "
+                   f"wgrad {line['wgrad_geomean_tflops']} TFLOP/s")
+    return "\n".join(out)
+
+
 def geomean(xs):
     return math.exp(sum(math.log(x) for x in xs) / len(xs))
 
@@ -212,7 +250,13 @@ def main():
                     help="summarize two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of "
                          "`bench.py --steps S --warmup W --no-cpu --copy-calibration` (same S, W, --shapes) "
                          "and exit; runs on the CPU")
+    ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "BENCH_JSON"),
+                    help="summarize a rocprofv3 --kernel-trace --stats run of the default bench "
+                         "(its kernel_stats.csv and the JSON line it printed) and exit; runs on the CPU")
     args = ap.parse_args()
+    if args.stats_summary:
+        print(stats_summary(*args.stats_summary))
+        return
     if args.pmc_summary:
         print(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.steps, args.warmup, args.shapes))
         return
@@ -288,7 +332,7 @@ def main():
                                   args.steps, args.warmup, flush)
             row["wgrad_us"] = med * 1e3
             row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
-            account("mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0>, true>", mean, flops)
+            account(WGRAD_KERNEL, mean, flops)
             del qg, qi, sg, si
         torch.cuda.empty_cache()
         rows.append(row)
