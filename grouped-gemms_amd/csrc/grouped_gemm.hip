@@ -572,8 +572,10 @@ struct ScaleJobs {
 };
 
 // 64 rows x 16 steps per workgroup (256 threads): each thread reads 16
-// source bytes of one row (4 steps), the tile is transposed through LDS, and
-// each thread writes 4 dwords of consecutive rows for one step.
+// source bytes of one row (4 steps; one 16-byte load when the chunk is
+// aligned and inside the row), the tile is transposed through LDS, and each
+// thread writes the dwords of 4 consecutive rows for one step (one 16-byte
+// store when aligned and inside the operand).
 __global__ __launch_bounds__(256) void scale_relayout_kernel(ScaleJobs js) {
   __shared__ uint32_t tile[16][65];
   int bid = blockIdx.x;
@@ -588,34 +590,45 @@ __global__ __launch_bounds__(256) void scale_relayout_kernel(ScaleJobs js) {
   {
     const int r = r0 + threadIdx.x / 4;
     const int tq = threadIdx.x % 4;                // steps t0 + 4 tq .. + 3
-    const uint8_t* row = J.src + (int64_t)b * J.ld_b + (int64_t)r * J.ld_r;
+    const int blk0 = 4 * t0 + 16 * tq;             // first scale byte of the chunk
+    uint32_t v[4] = {0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
+    if (r < J.rows && blk0 < J.nblk) {
+      const uint8_t* src = J.src + (int64_t)b * J.ld_b + (int64_t)r * J.ld_r + blk0;
+      if (blk0 + 16 <= J.nblk && ((uintptr_t)src & 15) == 0) {
+        const uint4 q = *(const uint4*)src;
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+      } else {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int t = t0 + 4 * tq + s;
-      uint32_t v = 0x7f7f7f7fu;
-      if (r < J.rows) {
-        v = 0;
+        for (int s = 0; s < 4; ++s) {
+          uint32_t w = 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int blk = 4 * t + q;
-          const uint32_t byte = blk < J.nblk ? (uint32_t)row[blk] : 127u;
-          v |= byte << (8 * q);
+          for (int q = 0; q < 4; ++q) {
+            const int i = 4 * s + q;
+            const uint32_t byte = blk0 + i < J.nblk ? (uint32_t)src[i] : 127u;
+            w |= byte << (8 * q);
+          }
+          v[s] = w;
         }
       }
-      tile[4 * tq + s][threadIdx.x / 4] = v;
     }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) tile[4 * tq + s][threadIdx.x / 4] = v[s];
   }
   __syncthreads();
   {
     const int ts = threadIdx.x / 16;               // step of the tile
     const int rq = threadIdx.x % 16;               // rows 4 rq .. 4 rq + 3
     const int t = t0 + ts;
-    if (t < J.steps) {
-      uint32_t* out = J.dst + ((int64_t)b * J.steps + t) * J.rows;
+    const int r = r0 + 4 * rq;
+    if (t < J.steps && r < J.rows) {
+      uint32_t* out = J.dst + ((int64_t)b * J.steps + t) * J.rows + r;
+      if (r + 4 <= J.rows && ((uintptr_t)out & 15) == 0) {
+        *(uint4*)out = make_uint4(tile[ts][4 * rq], tile[ts][4 * rq + 1], tile[ts][4 * rq + 2],
+                                  tile[ts][4 * rq + 3]);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = r0 + 4 * rq + q;
-        if (r < J.rows) out[r] = tile[ts][4 * rq + q];
+        for (int q = 0; q < 4; ++q)
+          if (r + q < J.rows) out[q] = tile[ts][4 * rq + q];
       }
     }
   }
