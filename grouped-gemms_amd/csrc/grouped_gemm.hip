@@ -38,6 +38,73 @@ constexpr int STEP = 128;      // reduction elements per scale dword (4 blocks o
 constexpr int SCG = 2;         // steps per scale group (one scale-ring slot)
 constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
 
+// Split of the last, partial round.  With T tiles and P workgroups resident
+// at once, the rem = T % P tiles of the last round leave most of the chip idle
+// for (a fraction of) a tile time.  They can instead be cut into S pieces
+// along the reduction (whole 128-element steps, at least kMinSplitSteps per
+// piece, at most kMaxSplit pieces per tile, S <= P / rem, `slots` pieces in
+// all); pieces store fp32 partial tiles and a second kernel adds them in
+// piece order and rounds once.  Tiles 0 .. dp-1 run whole, tile dp + v as
+// pieces v*S .. v*S+S-1.
+//
+// Only a last round that follows at most kSplitMaxRounds full rounds is
+// split: after more rounds the whole tiles finish at spread-out times, the
+// last round's tiles start early, and little idle time is left to recover
+// (measured: a loss from 5 full rounds on).  S is picked by a cost model
+// (microseconds, MI355X kernel traces): the last round of n steps costs about
+// kTailShare * n * kStepUs; cut into S pieces it costs n / S of that, plus
+// kSplitFixedUs (piece prologue and epilogue, two launches) plus the partial
+// traffic, rem * S tiles written and read back (kSplitUsPerMiB).  No split
+// unless that saves at least kSplitMinGainUs (the model is coarse);
+// reductions shorter than kMinSplitTotal steps are never split.
+constexpr int kMinSplitSteps = 4;
+constexpr int kMaxSplit = 8;
+constexpr int kMinSplitTotal = 32;
+constexpr int kSplitMaxRounds = 2;
+constexpr float kTailShare = 0.75f;
+constexpr float kStepUs = 1.7f;
+constexpr float kSplitFixedUs = 12.f;
+constexpr float kSplitUsPerMiB = 0.55f;
+constexpr float kSplitMinGainUs = 16.f;
+constexpr size_t kSplitBytes = (size_t)64 << 20;   // partial-tile area of a full workspace
+
+struct Split {
+  int dp;       // tiles computed whole
+  int S;        // pieces per split tile (1: no split)
+  int units;    // pieces in all (rem * S, or 0)
+};
+
+__host__ __device__ inline Split split_plan(int T, int P, int nsteps, int slots, int tile_kib) {
+  Split sp{T, 1, 0};
+  if (T <= 0 || P <= 0 || nsteps < kMinSplitTotal || T / P > kSplitMaxRounds) return sp;
+  const int rem = T % P;
+  if (rem == 0) return sp;
+  int smax = P / rem;
+  if (smax > kMaxSplit) smax = kMaxSplit;
+  if (smax > nsteps / kMinSplitSteps) smax = nsteps / kMinSplitSteps;
+  if (smax > slots / rem) smax = slots / rem;
+  const float tail = kTailShare * (float)nsteps * kStepUs;
+  float best = kSplitMinGainUs;
+  for (int S = 2; S <= smax; ++S) {
+    const float gain = tail * (1.f - 1.f / (float)S) - kSplitFixedUs -
+                       (float)(rem * S) * (float)tile_kib * (kSplitUsPerMiB / 1024.f);
+    if (gain > best) {
+      best = gain;
+      sp.S = S;
+    }
+  }
+  if (sp.S < 2) return sp;
+  sp.dp = T - rem;
+  sp.units = rem * sp.S;
+  return sp;
+}
+
+// Steps [a, b) of piece s out of S over steps [a0, a0 + n).
+__host__ __device__ inline void split_range(int a0, int n, int s, int S, int& a, int& b) {
+  a = a0 + (int)((int64_t)n * s / S);
+  b = a0 + (int)((int64_t)n * (s + 1) / S);
+}
+
 template <int BM_, int BN_, int WGM_, int WGN_, int WFMT_, int NS_>
 struct Cfg {
   static constexpr int BM = BM_;        // X rows per tile (output rows)
@@ -407,17 +474,63 @@ __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, c
   MXGG_WAIT_VM(0);
 }
 
+// Store 4 consecutive output columns c .. c+3 of row r (those below `cols`)
+// of a row-major output of element type out_dtype.  vec: rows and `out`
+// aligned for one 16-byte (f32) or 8-byte (16-bit) store of the four.
+// BF16_ONLY: round to bf16 first whatever the output type (wgrad semantics).
+template <bool BF16_ONLY>
+__device__ __forceinline__ void store4(uint8_t* out, int64_t ldo, int out_dtype, bool vec, int r, int c,
+                                       int cols, float v0, float v1, float v2, float v3) {
+  if (out_dtype == MXGG_DTYPE_F32) {
+    if (BF16_ONLY) {
+      v0 = round_bf16(v0); v1 = round_bf16(v1); v2 = round_bf16(v2); v3 = round_bf16(v3);
+    }
+    float* p = reinterpret_cast<float*>(out) + (int64_t)r * ldo + c;
+    if (vec && c + 3 < cols) {
+      *reinterpret_cast<float4*>(p) = make_float4(v0, v1, v2, v3);
+    } else {
+      if (c + 0 < cols) p[0] = v0;
+      if (c + 1 < cols) p[1] = v1;
+      if (c + 2 < cols) p[2] = v2;
+      if (c + 3 < cols) p[3] = v3;
+    }
+  } else {
+    uint32_t w0, w1;
+    if (out_dtype == MXGG_DTYPE_BF16) {
+      w0 = pack_bf16x2(v0, v1);
+      w1 = pack_bf16x2(v2, v3);
+    } else {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      h2 a = {(_Float16)v0, (_Float16)v1}, b = {(_Float16)v2, (_Float16)v3};
+      w0 = __builtin_bit_cast(uint32_t, a);
+      w1 = __builtin_bit_cast(uint32_t, b);
+    }
+    uint16_t* p = reinterpret_cast<uint16_t*>(out) + (int64_t)r * ldo + c;
+    if (vec && c + 3 < cols) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
+    } else {
+      if (c + 0 < cols) p[0] = (uint16_t)(w0 & 0xffff);
+      if (c + 1 < cols) p[1] = (uint16_t)(w0 >> 16);
+      if (c + 2 < cols) p[2] = (uint16_t)(w1 & 0xffff);
+      if (c + 3 < cols) p[3] = (uint16_t)(w1 >> 16);
+    }
+  }
+}
+
+__device__ __forceinline__ bool store4_vec(const uint8_t* out, int64_t ldo, int out_dtype) {
+  return out_dtype == MXGG_DTYPE_F32 ? ((ldo % 4) == 0 && ((uintptr_t)out % 16) == 0)
+                                     : ((ldo % 4) == 0 && ((uintptr_t)out % 8) == 0);
+}
+
 // Store an accumulator tile.  Lane l of fragment (i, j) holds output row
 // wm*WTM + 32i + l%32 and columns wn*WTN + 32j + 8(q/4) + 4(l/32) + q%4.
-// BF16_ONLY: round to bf16 first whatever the output type (wgrad semantics).
 template <class C, bool BF16_ONLY>
 __device__ __forceinline__ void store_tile(const v16f (&acc)[C::FM][C::FN], uint8_t* out,
                                            int64_t ldo, int rows, int cols, int out_dtype) {
   const int wave = wave_id();
   const int lane = threadIdx.x % kWave;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
-  const bool vec = out_dtype == MXGG_DTYPE_F32 ? ((ldo % 4) == 0 && ((uintptr_t)out % 16) == 0)
-                                               : ((ldo % 4) == 0 && ((uintptr_t)out % 8) == 0);
+  const bool vec = store4_vec(out, ldo, out_dtype);
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) {
     const int r = wm * C::WTM + i * 32 + (lane & 31);
@@ -427,45 +540,29 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[C::FM][C::FN], uint
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int c = wn * C::WTN + j * 32 + 8 * q4 + 4 * (lane >> 5);
-        float v0 = acc[i][j][4 * q4 + 0], v1 = acc[i][j][4 * q4 + 1];
-        float v2 = acc[i][j][4 * q4 + 2], v3 = acc[i][j][4 * q4 + 3];
-        if (out_dtype == MXGG_DTYPE_F32) {
-          if (BF16_ONLY) {
-            v0 = round_bf16(v0); v1 = round_bf16(v1); v2 = round_bf16(v2); v3 = round_bf16(v3);
-          }
-          float* p = reinterpret_cast<float*>(out) + (int64_t)r * ldo + c;
-          if (vec && c + 3 < cols) {
-            *reinterpret_cast<float4*>(p) = make_float4(v0, v1, v2, v3);
-          } else {
-            if (c + 0 < cols) p[0] = v0;
-            if (c + 1 < cols) p[1] = v1;
-            if (c + 2 < cols) p[2] = v2;
-            if (c + 3 < cols) p[3] = v3;
-          }
-        } else {
-          uint32_t w0, w1;
-          if (out_dtype == MXGG_DTYPE_BF16) {
-            w0 = pack_bf16x2(v0, v1);
-            w1 = pack_bf16x2(v2, v3);
-          } else {
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            h2 a = {(_Float16)v0, (_Float16)v1}, b = {(_Float16)v2, (_Float16)v3};
-            w0 = __builtin_bit_cast(uint32_t, a);
-            w1 = __builtin_bit_cast(uint32_t, b);
-          }
-          uint16_t* p = reinterpret_cast<uint16_t*>(out) + (int64_t)r * ldo + c;
-          if (vec && c + 3 < cols) {
-            *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
-          } else {
-            if (c + 0 < cols) p[0] = (uint16_t)(w0 & 0xffff);
-            if (c + 1 < cols) p[1] = (uint16_t)(w0 >> 16);
-            if (c + 2 < cols) p[2] = (uint16_t)(w1 & 0xffff);
-            if (c + 3 < cols) p[3] = (uint16_t)(w1 >> 16);
-          }
-        }
+        store4<BF16_ONLY>(out, ldo, out_dtype, vec, r, c, cols, acc[i][j][4 * q4 + 0], acc[i][j][4 * q4 + 1],
+                          acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
       }
     }
   }
+}
+
+// fp32 partial tile of a split unit, in accumulator-register order: the 16
+// values of lane l of fragment f = (wave * FM + i) * FN + j at floats
+// (f * 64 + l) * 16 .. +15 of the unit's BM x BN slot (whole-wave 4 KB runs).
+template <class C>
+__device__ __forceinline__ void store_partial(const v16f (&acc)[C::FM][C::FN], float* slot) {
+  const int wave = wave_id();
+  const int lane = threadIdx.x % kWave;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      float4* d = reinterpret_cast<float4*>(slot + ((int64_t)((wave * C::FM + i) * C::FN + j) * kWave + lane) * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        d[q] = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    }
 }
 
 // Store a 16-bit (bf16 / f16) accumulator tile through LDS so that every
@@ -645,36 +742,58 @@ struct FwdParams {
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype; int64_t ldo;
   int grid_n; int group_m; int xcd;
+  float* part; int par; int slots;          // split: partial slots, resident workgroups, slot count
 };
 
+struct FwdTile {
+  int expert;
+  int64_t row0; int rows;     // output rows row0 .. row0 + rows - 1 (one group)
+  int64_t n0; int cols;       // output columns n0 .. n0 + cols - 1
+};
+
+// Tile of logical index lt (0 <= lt < tiles) after the XCD swizzle and the
+// GROUP_M band order; false when it holds no output rows.  Wave-uniform.
 template <class C>
-__global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
-  const int pid = blockIdx.x;
-  const int total_m = route_total(p.offs, p.E, C::BM);
-  const int tiles = total_m * p.grid_n;
-  if (pid >= tiles) return;
-  const int t = p.xcd > 1 ? xcd_swizzle(pid, tiles, p.xcd) : pid;
+__device__ __forceinline__ bool fwd_tile(const FwdParams& p, int lt, int tiles, int total_m, FwdTile& tl) {
+  const int t = p.xcd > 1 ? xcd_swizzle(lt, tiles, p.xcd) : lt;
   int pm, pn;
   pid_grid(t, total_m, p.grid_n, p.group_m, pm, pn);
   const TileRoute r = route_find(p.offs, p.E, C::BM, pm);
-  if (r.expert < 0) return;
-  const int64_t row0 = (int64_t)r.start + (int64_t)r.block * C::BM;
-  int64_t rows64 = p.M - row0;
+  if (r.expert < 0) return false;
+  tl.expert = r.expert;
+  tl.row0 = (int64_t)r.start + (int64_t)r.block * C::BM;
+  int64_t rows64 = p.M - tl.row0;
   if (rows64 > r.rows) rows64 = r.rows;
-  if (rows64 <= 0) return;
-  const int rows = (int)rows64;
-  const int64_t n0 = (int64_t)pn * C::BN;
-  const int cols = (int)(p.N - n0 < C::BN ? p.N - n0 : C::BN);
+  if (rows64 <= 0) return false;
+  tl.rows = (int)rows64;
+  tl.n0 = (int64_t)pn * C::BN;
+  tl.cols = (int)(p.N - tl.n0 < C::BN ? p.N - tl.n0 : C::BN);
+  return true;
+}
+
+template <class C>
+__device__ __forceinline__ Split fwd_split(const FwdParams& p, int tiles) {
+  return split_plan(tiles, p.par, (int)((p.K + STEP - 1) / STEP), p.slots, C::BM * C::BN * 4 / 1024);
+}
+
+// Tile lt whole (PIECES = false), or piece `piece` of S of it into partial
+// slot `slot` (PIECES = true).
+template <class C, bool PIECES>
+__device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int lt, int piece, int S, int slot,
+                                        int tiles, int total_m) {
+  FwdTile tl;
+  if (!fwd_tile<C>(p, lt, tiles, total_m, tl)) return;
+  const int64_t row0 = tl.row0, n0 = tl.n0;
+  const int rows = tl.rows, cols = tl.cols;
 
   Operand X, W;
   X.ld = (uint32_t)p.lda;
   X.data = make_rsrc(p.a + row0 * p.lda, (uint32_t)rows * X.ld);
   W.ld = (uint32_t)p.ldb_n;
-  W.data = make_rsrc(p.b + (int64_t)r.expert * p.ldb_e + n0 * p.ldb_n, (uint32_t)cols * W.ld);
+  W.data = make_rsrc(p.b + (int64_t)tl.expert * p.ldb_e + n0 * p.ldb_n, (uint32_t)cols * W.ld);
   const uint32_t T = (uint32_t)((p.K + STEP - 1) / STEP);
   const ScaleSrc xs{0u, (uint32_t)p.M, (uint32_t)row0};
-  const ScaleSrc ws{4u * T * ((uint32_t)p.M + (uint32_t)r.expert * (uint32_t)p.N), (uint32_t)p.N, (uint32_t)n0};
+  const ScaleSrc ws{4u * T * ((uint32_t)p.M + (uint32_t)tl.expert * (uint32_t)p.N), (uint32_t)p.N, (uint32_t)n0};
   const __amdgpu_buffer_rsrc_t wsr = make_rsrc(p.ws, p.ws_bytes);
 
   v16f acc[C::FM][C::FN];
@@ -684,14 +803,107 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 
   const int K = (int)p.K;
-  ring_mainloop<C>(smem, X, W, wsr, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
+  if constexpr (PIECES) {
+    int a, b;
+    split_range(0, (int)T, piece, S, a, b);
+    const int lo = STEP * a;
+    const int hi = STEP * b < K ? STEP * b : K;
+    ring_mainloop<C>(smem, X, W, wsr, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
+    store_partial<C>(acc, p.part + (int64_t)slot * (C::BM * C::BN));
+  } else {
+    ring_mainloop<C>(smem, X, W, wsr, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
+    const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
+    uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
+    if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
+      store_tile_lds<C>(acc, smem, o, p.ldo, rows, cols, p.out_dtype);
+    else
+      store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
+  }
+}
 
+// PIECES = false: workgroup i < dp computes tile i whole.  PIECES = true:
+// workgroup u < units computes piece u % S of tile dp + u / S into partial
+// slot u.  Other workgroups exit.  (Two kernels rather than one with both
+// paths: sharing a register allocation slows the whole-tile loop by ~2%.)
+template <class C, bool PIECES>
+__global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+  const int total_m = route_total(p.offs, p.E, C::BM);
+  const int tiles = total_m * p.grid_n;
+  const Split sp = fwd_split<C>(p, tiles);
+  const int pid = blockIdx.x;
+  if constexpr (PIECES) {
+    if (pid < sp.units) fwd_run<C, true>(p, smem, sp.dp + pid / sp.S, pid % sp.S, sp.S, pid, tiles, total_m);
+  } else {
+    if (pid < sp.dp) fwd_run<C, false>(p, smem, pid, 0, 1, 0, tiles, total_m);
+  }
+}
+
+// Sum over the S pieces (slots base + s * BM * BN, s = 0 .. S-1, in that
+// order) of the 16 partial values of lane `lane` of fragment f.
+template <class C>
+__device__ __forceinline__ void sum_pieces(const float* base, int S, int f, int lane, float (&v)[16]) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) v[q] = 0.f;
+  const float* src = base + ((int64_t)f * kWave + lane) * 16;
+  for (int s = 0; s < S; ++s) {
+    const float4* x = reinterpret_cast<const float4*>(src + (int64_t)s * (C::BM * C::BN));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 t = x[q];
+      v[4 * q] += t.x; v[4 * q + 1] += t.y; v[4 * q + 2] += t.z; v[4 * q + 3] += t.w;
+    }
+  }
+}
+
+// Store the 16 values of lane `lane` of fragment f of a tile (rows x cols at
+// `out`, row stride ldo).
+template <class C, bool BF16_ONLY>
+__device__ __forceinline__ void store_fragment_lane(const float (&v)[16], int f, int lane, uint8_t* out,
+                                                    int64_t ldo, int rows, int cols, int out_dtype) {
+  const int wave = f / (C::FM * C::FN), i = (f / C::FN) % C::FM, j = f % C::FN;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int r = wm * C::WTM + i * 32 + (lane & 31);
+  if (r >= rows) return;
+  const bool vec = store4_vec(out, ldo, out_dtype);
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const int c = wn * C::WTN + j * 32 + 8 * q4 + 4 * (lane >> 5);
+    store4<BF16_ONLY>(out, ldo, out_dtype, vec, r, c, cols, v[4 * q4], v[4 * q4 + 1], v[4 * q4 + 2], v[4 * q4 + 3]);
+  }
+}
+
+// Fragments per tile and reduce items per tile (4 fragments, one per wave of
+// a 256-thread workgroup).
+template <class C>
+struct ReduceShape {
+  static constexpr int NF = C::NW * C::FM * C::FN;
+  static constexpr int CH = NF / 4;
+  static_assert(NF % 4 == 0, "reduce items");
+};
+
+// Split tiles of a forward launch: item (v, c) = fragments 4c .. 4c+3 of split
+// tile v, summed over its pieces and stored.  The plan is recomputed from
+// offs exactly as fwd_kernel computed it.
+template <class C>
+__global__ __launch_bounds__(256) void fwd_reduce_kernel(FwdParams p) {
+  const int total_m = route_total(p.offs, p.E, C::BM);
+  const int tiles = total_m * p.grid_n;
+  const Split sp = fwd_split<C>(p, tiles);
+  if (sp.units == 0) return;
+  constexpr int CH = ReduceShape<C>::CH;
+  const int rem = sp.units / sp.S;
+  const int lane = threadIdx.x % kWave;
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-  uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
-  if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
-    store_tile_lds<C>(acc, smem, o, p.ldo, rows, cols, p.out_dtype);
-  else
-    store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
+  for (int item = blockIdx.x; item < rem * CH; item += gridDim.x) {
+    const int v = item / CH, f = (item % CH) * 4 + wave_id();
+    FwdTile tl;
+    if (!fwd_tile<C>(p, sp.dp + v, tiles, total_m, tl)) continue;
+    float acc[16];
+    sum_pieces<C>(p.part + (int64_t)v * sp.S * (C::BM * C::BN), sp.S, f, lane, acc);
+    store_fragment_lane<C, false>(acc, f, lane, p.out + (tl.row0 * p.ldo + tl.n0) * esz, p.ldo, tl.rows,
+                                  tl.cols, p.out_dtype);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -706,21 +918,58 @@ struct WgradParams {
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype;
   int tiles_n; int tiles_k;
+  float* part; int dp; int S; int units;    // split plan (host): see split_plan
+};
+
+struct WgradTile {
+  int g;                      // group
+  int64_t n0; int rows;       // output rows (n) n0 .. n0 + rows - 1
+  int64_t k0; int cols;       // output columns (k) k0 .. k0 + cols - 1
 };
 
 template <class C>
+__device__ __forceinline__ WgradTile wgrad_tile(const WgradParams& p, int lt) {
+  WgradTile t;
+  const int per = p.tiles_n * p.tiles_k;
+  t.g = lt / per;
+  const int x = lt % per;
+  t.n0 = (int64_t)(x / p.tiles_k) * C::BM;   // X side: rows of go_t
+  t.k0 = (int64_t)(x % p.tiles_k) * C::BN;   // W side: rows of ia_t
+  t.rows = (int)(p.N - t.n0 < C::BM ? p.N - t.n0 : C::BM);
+  t.cols = (int)(p.K - t.k0 < C::BN ? p.K - t.k0 : C::BN);
+  return t;
+}
+
+// PIECES = false: grid (tiles_n * tiles_k, E), workgroup (x, g) computes tile
+// g * tiles_n * tiles_k + x whole when below dp; true: workgroup u computes
+// piece u % S of tile dp + u / S.
+template <class C, bool PIECES>
 __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
-  const int g = blockIdx.y;
-  const int tn = blockIdx.x / p.tiles_k;       // X side: rows of go_t (output rows n)
-  const int tk = blockIdx.x % p.tiles_k;       // W side: rows of ia_t (output cols k)
+  int lt, piece = 0;
+  if constexpr (PIECES) {
+    lt = p.dp + (int)blockIdx.x / p.S;
+    piece = (int)blockIdx.x % p.S;
+  } else {
+    lt = (int)blockIdx.y * p.tiles_n * p.tiles_k + (int)blockIdx.x;
+    if (lt >= p.dp) return;
+  }
+  const WgradTile tl = wgrad_tile<C>(p, lt);
+  const int g = tl.g;
+  const int64_t n0 = tl.n0, k0 = tl.k0;
+  const int rows = tl.rows, cols = tl.cols;
   int lo = g > 0 ? p.offs[g - 1] : 0;
   int hi = p.offs[g];
   if (lo < 0) lo = 0;
   if (hi > p.M) hi = (int)p.M;
-  const int64_t n0 = (int64_t)tn * C::BM, k0 = (int64_t)tk * C::BN;
-  const int rows = (int)(p.N - n0 < C::BM ? p.N - n0 : C::BM);
-  const int cols = (int)(p.K - k0 < C::BN ? p.K - k0 : C::BN);
+  if (PIECES && hi > lo) {
+    // piece of the group's steps lo/STEP .. cdiv(hi, STEP)-1, clipped to [lo, hi)
+    const int a0 = lo / STEP;
+    int a, b;
+    split_range(a0, (hi + STEP - 1) / STEP - a0, piece, p.S, a, b);
+    if (STEP * a > lo) lo = STEP * a;
+    if (STEP * b < hi) hi = STEP * b;
+  }
 
   Operand X, W;
   X.ld = (uint32_t)p.ld_go;
@@ -740,12 +989,31 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 
   if (hi > lo) ring_mainloop<C>(smem, X, W, wsr, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
 
+  if constexpr (PIECES) {
+    store_partial<C>(acc, p.part + (int64_t)blockIdx.x * (C::BM * C::BN));
+    return;
+  }
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
   if (esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
     store_tile_lds<C>(acc, smem, o, p.K, rows, cols, p.out_dtype);
   else
     store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
+}
+
+// Split tiles of a wgrad launch: one workgroup per item (v, c), as in
+// fwd_reduce_kernel; the grid is exact (the plan is the host's).
+template <class C>
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
+  constexpr int CH = ReduceShape<C>::CH;
+  const int v = blockIdx.x / CH, f = (blockIdx.x % CH) * 4 + wave_id();
+  const int lane = threadIdx.x % kWave;
+  const WgradTile tl = wgrad_tile<C>(p, p.dp + v);
+  float acc[16];
+  sum_pieces<C>(p.part + (int64_t)v * p.S * (C::BM * C::BN), p.S, f, lane, acc);
+  const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
+  store_fragment_lane<C, true>(acc, f, lane, p.out + ((int64_t)tl.g * p.N * p.K + tl.n0 * p.K + tl.k0) * esz,
+                               p.K, tl.rows, tl.cols, p.out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -825,16 +1093,75 @@ FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, in
   return c;
 }
 
+// Workgroups of `kernel` (nt threads) resident on the current device at
+// once: CUs x per-CU occupancy (LDS, registers).  Cached per device.
+template <class KF>
+int resident_workgroups(KF kernel, int nt, int (&cache)[64]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64 && cache[dev]) return cache[dev];
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, nt, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int r = cus * (per > 0 ? per : 1);
+  if (dev >= 0 && dev < 64) cache[dev] = r;
+  return r;
+}
+
 template <class C>
-int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, hipStream_t st) {
+int fwd_resident() {
+  static int cache[64];
+  return resident_workgroups(fwd_kernel<C, false>, C::NT, cache);
+}
+
+// Partial slots of BM x BN fp32 available in `bytes` (capped).
+template <class C>
+int split_slots(size_t bytes) {
+  const size_t n = bytes / ((size_t)C::BM * C::BN * 4);
+  return n > 4096 ? 4096 : (int)n;
+}
+
+// Forward launch: the whole tiles (grid: every possible tile; those at or
+// past dp exit), then, when the workspace allows a split at all, the pieces
+// (grid: the most pieces a plan can have) and the reduce of the split tiles.
+// The plan itself depends on offs and is made on the device.
+template <class C>
+int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_bytes, hipStream_t st) {
   FwdParams p = p0;
   p.grid_n = (int)cdiv(p.N, C::BN);
   p.group_m = gm;
   p.xcd = xcd;
-  const int64_t grid = (int64_t)grid_m_ub * p.grid_n;
-  if (grid <= 0) return MXGG_OK;
-  if (grid > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
-  hipLaunchKernelGGL((fwd_kernel<C>), dim3((unsigned)grid), dim3(C::NT), 0, st, p);
+  p.par = fwd_resident<C>();
+  p.slots = p.part ? split_slots<C>(part_bytes) : 0;
+  const int nsteps = (int)cdiv(p.K, STEP);
+  if (p.par <= 0 || p.slots < 2 || nsteps < kMinSplitTotal) p.slots = 0;
+  // Rows of every group add up to M in the usual MoE call, with half a tile
+  // of padding per group on average: when the plan for that many tiles does
+  // not split, the piece and reduce launches are skipped (p.slots = 0 makes
+  // the device plan agree).  A wrong guess costs time, never correctness.
+  if (p.slots) {
+    const int64_t est = (cdiv(p.M, C::BM) + (p.E - 1) / 2) * p.grid_n;
+    if (est > INT32_MAX || split_plan((int)est, p.par, nsteps, p.slots, C::BM * C::BN * 4 / 1024).units == 0)
+      p.slots = 0;
+  }
+  const int64_t tiles_ub = (int64_t)grid_m_ub * p.grid_n;
+  if (tiles_ub <= 0) return MXGG_OK;
+  if (tiles_ub > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
+  hipLaunchKernelGGL((fwd_kernel<C, false>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
+  if (int rc = launch_status("grouped_mm")) return rc;
+  if (!p.slots) return MXGG_OK;
+  const int pieces = p.slots < p.par ? p.slots : p.par;   // units <= min(slots, P)
+  hipLaunchKernelGGL((fwd_kernel<C, true>), dim3((unsigned)pieces), dim3(C::NT), 0, st, p);
+  if (int rc = launch_status("grouped_mm")) return rc;
+  // a split needs rem <= par / 2 tiles of ReduceShape::CH items each; a small
+  // grid loops over them (and costs little when the plan has no split)
+  const int64_t items = (int64_t)(p.par / 2) * ReduceShape<C>::CH;
+  const int64_t rgrid = items < 128 ? items : 128;
+  if (rgrid <= 0) return MXGG_OK;
+  hipLaunchKernelGGL((fwd_reduce_kernel<C>), dim3((unsigned)rgrid), dim3(256), 0, st, p);
   return launch_status("grouped_mm");
 }
 
@@ -902,9 +1229,33 @@ extern "C" int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t
 
 static bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Re-laid scales of a forward call: A [T][M], then B [E][T][N] dwords.
+static size_t fwd_scale_bytes(int E, int64_t M, int64_t N, int64_t K) {
+  return (size_t)4 * (size_t)cdiv(K, STEP) * ((size_t)M + (size_t)E * (size_t)N);
+}
+
+// Partial-tile area worth reserving: up to kSplitBytes, no more than `tiles`
+// tiles of `tile_bytes` cut into the most pieces a reduction of `nsteps`
+// steps allows.
+static size_t split_area(int64_t tiles, size_t tile_bytes, int64_t nsteps) {
+  if (nsteps < kMinSplitTotal || tiles <= 0) return 0;
+  int64_t smax = nsteps / kMinSplitSteps;
+  if (smax > kMaxSplit) smax = kMaxSplit;
+  const double want = (double)tiles * (double)smax * (double)tile_bytes;
+  return want < (double)kSplitBytes ? (size_t)want : kSplitBytes;
+}
+
 extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
   if (E <= 0 || M < 0 || N < 0 || K < 0) return 0;
-  return (size_t)4 * (size_t)cdiv(K, STEP) * ((size_t)M + (size_t)E * (size_t)N);
+  const size_t sc = fwd_scale_bytes(E, M, N, K);
+  if (sc == 0 || M == 0 || N == 0) return sc;
+  const int64_t nsteps = cdiv(K, STEP);
+  const size_t a = split_area((cdiv(M, 256) + E - 1) * cdiv(N, 256), (size_t)256 * 256 * 4, nsteps);
+  const size_t b = split_area((cdiv(M, 128) + E - 1) * cdiv(N, 128), (size_t)128 * 128 * 4, nsteps);
+  const size_t part = a > b ? a : b;
+  return part ? align256(sc) + part : sc;
 }
 
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
@@ -935,10 +1286,10 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   if (M == 0 || N == 0) return MXGG_OK;
   if (!A || !A_s || !B || !B_s || !offs || !out)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: null pointer");
-  const size_t need = mxgg_grouped_mm_workspace_size(E, M, N, K);
+  const size_t need = fwd_scale_bytes(E, M, N, K);
   if (need >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: problem too large");
   if (need && (!workspace || ws_bytes < need))
-    return fail(MXGG_ERR_WORKSPACE, "grouped_mm: workspace of %zu bytes needed, %zu given", need,
+    return fail(MXGG_ERR_WORKSPACE, "grouped_mm: workspace of at least %zu bytes needed, %zu given", need,
                 workspace ? ws_bytes : (size_t)0);
   if (int rc = require_device()) return rc;
   FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
@@ -954,13 +1305,17 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
                                  "grouped_mm"))
       return rc;
   }
+  // partial tiles of a split last round after the scales (optional)
+  const size_t part_off = align256(need);
+  float* part = ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
+  const size_t part_bytes = part ? ws_bytes - part_off : 0;
   FwdParams p{A, lda, B, ldb_n, ldb_e, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
-              (uint8_t*)out, out_dtype, ldo, 0, 0, 0};
+              (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0};
   if (b_fmt == MXGG_FMT_E2M1)
-    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, st);
+    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, part_bytes, st);
   if (c.bm == 256)
-    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, st);
-  return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, st);
+    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, part_bytes, st);
+  return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, part_bytes, st);
 }
 
 extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,
@@ -981,10 +1336,24 @@ extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, in
   return MXGG_OK;
 }
 
-extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
-  (void)E;
-  if (M < 0 || N < 0 || K < 0) return 0;
+// Re-laid scales of a wgrad call: GO [T][N], then IA [T][K] dwords.
+static size_t wgrad_scale_bytes(int64_t M, int64_t N, int64_t K) {
   return (size_t)4 * (size_t)cdiv(M, STEP) * ((size_t)N + (size_t)K);
+}
+
+// Reduction steps of an average group (what the split plan is sized for).
+static int64_t wgrad_group_steps(int E, int64_t M) {
+  const int64_t n = cdiv(M, (int64_t)E * STEP);
+  return n > 0 ? n : 1;
+}
+
+extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
+  if (E <= 0 || M < 0 || N < 0 || K < 0) return 0;
+  const size_t sc = wgrad_scale_bytes(M, N, K);
+  if (sc == 0 || N == 0 || K == 0) return sc;
+  const size_t part = split_area((int64_t)E * cdiv(N, 256) * cdiv(K, 256), (size_t)256 * 256 * 4,
+                                 wgrad_group_steps(E, M));
+  return part ? align256(sc) + part : sc;
 }
 
 extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
@@ -1008,10 +1377,10 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   if (N == 0 || K == 0) return MXGG_OK;
   if (!go_t || !go_s || !ia_t || !ia_s || !offs || !out)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: null pointer");
-  const size_t need = mxgg_wgrad_workspace_size(E, M, N, K);
+  const size_t need = wgrad_scale_bytes(M, N, K);
   if (need >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: problem too large");
   if (need && (!workspace || ws_bytes < need))
-    return fail(MXGG_ERR_WORKSPACE, "wgrad: workspace of %zu bytes needed, %zu given", need,
+    return fail(MXGG_ERR_WORKSPACE, "wgrad: workspace of at least %zu bytes needed, %zu given", need,
                 workspace ? ws_bytes : (size_t)0);
   if (int rc = require_device()) return rc;
   typedef CfgF8_256 C;
@@ -1023,11 +1392,29 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
                                  scale_job(ia_s, ld_ias, 0, wsd + T * N, K, 1, M / 32, T), st, "wgrad"))
       return rc;
   }
+  const size_t part_off = align256(need);
+  float* part = ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
   WgradParams p{go_t, ld_go, ia_t, ld_ia, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
-                (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN)};
-  const int64_t gx = (int64_t)p.tiles_n * p.tiles_k;
-  if (gx > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");
-  dim3 grid((unsigned)gx, (unsigned)E);
-  hipLaunchKernelGGL((wgrad_kernel<C>), grid, dim3(C::NT), 0, st, p);
+                (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0};
+  const int64_t tiles = (int64_t)E * p.tiles_n * p.tiles_k;
+  if (tiles > INT32_MAX / 2) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");
+  static int resident_cache[64];
+  const int par = resident_workgroups(wgrad_kernel<C, false>, C::NT, resident_cache);
+  // groups differ in length, and with them the tiles' run times: with E > 1
+  // only a lone under-filled round is split (its tiles all start at once)
+  const bool may_split = E == 1 || tiles < par;
+  const int slots = part && may_split ? split_slots<C>(ws_bytes - part_off) : 0;
+  const Split sp = split_plan((int)tiles, par, (int)wgrad_group_steps(E, M), slots, C::BM * C::BN * 4 / 1024);
+  p.dp = sp.dp;
+  p.S = sp.S;
+  p.units = sp.units;
+  hipLaunchKernelGGL((wgrad_kernel<C, false>), dim3((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E),
+                     dim3(C::NT), 0, st, p);
+  if (int rc = launch_status("wgrad")) return rc;
+  if (!sp.units) return MXGG_OK;
+  hipLaunchKernelGGL((wgrad_kernel<C, true>), dim3((unsigned)sp.units), dim3(C::NT), 0, st, p);
+  if (int rc = launch_status("wgrad")) return rc;
+  hipLaunchKernelGGL((wgrad_reduce_kernel<C>), dim3((unsigned)(sp.units / sp.S * ReduceShape<C>::CH)),
+                     dim3(256), 0, st, p);
   return launch_status("wgrad");
 }

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_VERSION 2000 /* major*1000 + minor */
+#define MXGG_VERSION 2001 /* major*1000 + minor */
 
 /* status codes */
 #define MXGG_OK 0
@@ -137,13 +137,18 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            written (as in the reference).
  *   block_m, block_n, group_m, xcd_swizzle: 0 = library choice; otherwise a
  *            request honoured when the build has that tile shape.
- *   workspace / ws_bytes: device scratch of at least
- *            mxgg_grouped_mm_workspace_size(E, M, N, K) bytes (4 * ceil(K/128) *
- *            (M + E*N)): the scales re-laid step-major for the kernel (the
- *            reference re-lays them per call too, kernels/forward.py:537-550).
- *            Its contents need not be initialised and are overwritten.
+ *   workspace / ws_bytes: device scratch, contents need not be initialised
+ *            and are overwritten.  Required: 4 * ceil(K/128) * (M + E*N) bytes,
+ *            the scales re-laid step-major for the kernel (the reference re-lays
+ *            them per call too, kernels/forward.py:537-550).  Recommended:
+ *            mxgg_grouped_mm_workspace_size(E, M, N, K) bytes, which adds (after
+ *            the scales, 256-byte aligned) room for the fp32 partial tiles of a
+ *            last, partial round of tiles cut along K (at most 64 MiB; only for
+ *            K >= 4096 and short launches).  With less, no tile is cut.
  * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
- * rows need no alignment.
+ * rows need no alignment.  Results do not depend on the workspace size beyond
+ * fp32 summation order (a cut tile adds its pieces in a fixed order, so
+ * repeated calls give identical bits).
  */
 size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
@@ -163,9 +168,12 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
  *   ia_t  (K, M) e4m3, row stride ld_ia;   ia_s (K, M/32), row stride ld_ias
  *   offs  (E,) int32 cumulative group ends, multiples of 32, offs[E-1] <= M
  *   out   (E, N, K) of out_dtype (BF16 or F32), contiguous
- *   workspace / ws_bytes: device scratch of at least
- *         mxgg_wgrad_workspace_size(E, M, N, K) bytes (4 * ceil(M/128) * (N + K)):
- *         the scales re-laid step-major; need not be initialised
+ *   workspace / ws_bytes: device scratch, need not be initialised.  Required:
+ *         4 * ceil(M/128) * (N + K) bytes (the scales re-laid step-major);
+ *         recommended: mxgg_wgrad_workspace_size(E, M, N, K), which adds room
+ *         for the fp32 partial tiles of tiles cut along the token range when
+ *         the tiles do not fill the chip (E = 1, or fewer tiles than
+ *         resident workgroups).
  */
 size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
