@@ -14,9 +14,9 @@
 // an NS-deep LDS ring.  While stage s is multiplied out of registers, stage
 // s+1 is read from LDS and stages s+2 .. s+NS are in flight, so the copies of
 // a stage have NS-1 stage times to land and the copy engine always has
-// several stages queued.  (An LDS-DMA copy costs about the same per
-// instruction whatever its row length, so shorter stages cost nothing extra
-// while deeper queues hide the memory latency.)
+// several stages queued.  (The two 64-byte halves of a 128-byte line, copied
+// a stage apart, move at ~80% of the full-line rate; copying stages in pairs
+// recovers the rate but shortens the prefetch, and measured slower.)
 //   * X and W tiles go global -> LDS directly with 16-byte buffer_load ... lds;
 //     chunks outside the reduction range read as zero through the buffer
 //     range check.  LDS rows are 64 bytes (e4m3) or 32 bytes (packed e2m1)
@@ -1408,9 +1408,11 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   p.dp = sp.dp;
   p.S = sp.S;
   p.units = sp.units;
-  hipLaunchKernelGGL((wgrad_kernel<C, false>), dim3((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E),
-                     dim3(C::NT), 0, st, p);
-  if (int rc = launch_status("wgrad")) return rc;
+  if (sp.dp > 0) {
+    hipLaunchKernelGGL((wgrad_kernel<C, false>), dim3((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E),
+                       dim3(C::NT), 0, st, p);
+    if (int rc = launch_status("wgrad")) return rc;
+  }
   if (!sp.units) return MXGG_OK;
   hipLaunchKernelGGL((wgrad_kernel<C, true>), dim3((unsigned)sp.units), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("wgrad")) return rc;
