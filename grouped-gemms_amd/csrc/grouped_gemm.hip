@@ -1081,11 +1081,17 @@ struct FwdChoice {
   int bm, bn, group_m, xcd;
 };
 
+// 256 x 256 tiles with GROUP_M 8 and the 8-XCD swizzle (best on every sweep
+// shape measured, the 2048 x 2048 ones included); 128 x 128 tiles for e4m3
+// problems too small to fill half the chip with 256 x 256 tiles and too
+// short (K < 4096) for the split of the last round to make up for it.
 FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, int bn, int gm,
                    int xcd) {
-  (void)E; (void)M; (void)K;
   FwdChoice c{256, 256, 8, 8};
-  if (b_fmt == MXGG_FMT_E4M3 && N <= 2048 && K <= 2048) { c.bm = 128; c.bn = 128; }
+  if (b_fmt == MXGG_FMT_E4M3 && K < 4096 && (cdiv(M, 256) + E - 1) * cdiv(N, 256) < 128) {
+    c.bm = 128;
+    c.bn = 128;
+  }
   if (bm) c.bm = bm;
   if (bn) c.bn = bn;
   if (gm) c.group_m = gm;

@@ -55,8 +55,13 @@ def test_launch_config_query():
     big = _pick_config(8, 16640, 8192, 8192)
     assert (big["BLOCK_M"], big["BLOCK_N"], big["BLOCK_K"]) == (256, 256, 128)
     assert big["GROUP_M"] > 0 and big["XCD_SWIZZLE"] == 8
-    small = _pick_config(1, 16640, 2048, 2048)
+    # the sweep's smallest shape fills the chip with 256 x 256 tiles (65 x 8 of them)
+    assert _pick_config(1, 16640, 2048, 2048)["BLOCK_M"] == 256
+    # 4 x 2 tiles of 256 would leave most CUs idle: 128 x 128 (7 x 4 expert-padded tiles)
+    small = _pick_config(4, 1024, 512, 512)
     assert (small["BLOCK_M"], small["BLOCK_N"]) == (128, 128)
+    # ... unless K is long enough for the split of the last round
+    assert _pick_config(4, 1024, 512, 8192)["BLOCK_M"] == 256
     assert _pick_config(1, 16640, 2048, 2048, b_fmt=_lib.FMT_E2M1)["BLOCK_M"] == 256
     req = _pick_config(1, 16640, 8192, 8192, BLOCK_M=128, BLOCK_N=128, GROUP_M=4, XCD_SWIZZLE=1)
     assert (req["BLOCK_M"], req["BLOCK_N"], req["GROUP_M"], req["XCD_SWIZZLE"]) == (128, 128, 4, 1)
