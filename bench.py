@@ -9,7 +9,9 @@ with jagged offsets drawn exactly like the reference's bench (random.seed(123),
 ``generate_jagged_offs`` in config order; bench.py:113-122, 250-257).  Inputs
 are synthetic (A, grad_out ~ N(0,1), weights ~ N(0,0.02)), quantized on the GPU
 before timing; quantization is outside the timed region, as in the reference
-(bench.py:126-130).
+(bench.py:126-130).  Beside the forward, the bf16 arm times torch._grouped_mm
+on the unquantized operands (reference bench.py:159-161) for the speedup the
+reference's README quotes (1.389x geomean MXFP8 vs bf16, README.md:80).
 
 Timed region per shape: the full drop-in Python call (output allocation, the
 C-ABI call, the in-kernel routing and the GEMM), bracketed by HIP events on
@@ -39,6 +41,7 @@ sys.path.insert(0, os.path.join(ROOT, "grouped-gemms_amd"))
 
 PEAK_MXFP8_TFLOPS = 5000.0          # MI355X published dense MXFP8 / FP8 peak
 REF_FWD_GEOMEAN_TFLOPS = 1498.8     # reference README table, 36-shape fwd geomean (MI355X)
+REF_SPEEDUP_VS_BF16 = 1.389         # reference README, geomean MXFP8 / bf16 torch._grouped_mm (MI355X)
 M_TOKENS = 16640
 SHAPES = [(e, n, k) for e, n, k in itertools.product((1, 2, 4, 8), (2048, 5120, 8192), (2048, 5120, 8192))]
 
@@ -249,6 +252,8 @@ def main():
     ap.add_argument("--shapes", type=int, default=36, help="first N shapes of the sweep")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-bf16", action="store_true",
+                    help="skip the bf16 torch._grouped_mm arm of the forward (reference bench.py:159-161)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 256 MiB device copies (PMC byte-counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -308,11 +313,23 @@ def main():
             w = (torch.randn((E, N, K), device=dev) * 0.02).to(torch.bfloat16)
             sa, qa = to_mx(a)
             sw, qw = to_mx(w)
+            if not args.no_bf16:
+                # bf16 arm: torch's grouped GEMM on the unquantized operands, as the
+                # reference's bench does (bench.py:159-161); weights given as a
+                # contiguous (E, K, N) tensor rather than a transposed view
+                wk = w.transpose(-2, -1).contiguous()
+                bmed, _ = time_call(lambda: torch._grouped_mm(a, wk, offs, out_dtype=torch.bfloat16),
+                                    args.steps, args.warmup, flush)
+                row["bf16_us"] = bmed * 1e3
+                row["bf16_tflops"] = flops / (bmed * 1e-3) / 1e12
+                del wk
             del a, w
             med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs),
                                   args.steps, args.warmup, flush)
             row["fwd_us"] = med * 1e3
             row["fwd_tflops"] = flops / (med * 1e-3) / 1e12
+            if "bf16_us" in row:
+                row["fwd_speedup_vs_bf16"] = row["bf16_us"] / row["fwd_us"]
             account(fwd_kernel_name(_pick_config(E, M, N, K)), mean, flops)
             del qa, qw, sa, sw
         if args.only in ("all", "dgrad"):
@@ -348,6 +365,7 @@ def main():
         return geomean(vals) if vals else None
 
     fwd_gm, dgrad_gm, wgrad_gm = gm("fwd_tflops"), gm("dgrad_tflops"), gm("wgrad_tflops")
+    bf16_gm, speedup_gm = gm("bf16_tflops"), gm("fwd_speedup_vs_bf16")
     ms_per_step = sum(r.get("fwd_us", 0) + r.get("dgrad_us", 0) + r.get("wgrad_us", 0) for r in rows) / 1e3
     per_e = {}
     for e in (1, 2, 4, 8):
@@ -393,6 +411,9 @@ def main():
         "dgrad_geomean_tflops": round(dgrad_gm, 1) if dgrad_gm else None,
         "wgrad_geomean_tflops": round(wgrad_gm, 1) if wgrad_gm else None,
         "fwd_pct_of_peak": round(100 * fwd_gm / PEAK_MXFP8_TFLOPS, 2) if fwd_gm else None,
+        "bf16_fwd_geomean_tflops": round(bf16_gm, 1) if bf16_gm else None,
+        "fwd_speedup_vs_bf16_geomean": round(speedup_gm, 3) if speedup_gm else None,
+        "ref_speedup_vs_bf16_geomean": REF_SPEEDUP_VS_BF16,
         "fwd_geomean_by_E": per_e,
         "baseline_note": "vs_baseline = fwd geomean / 1498.8 TFLOP/s (reference README table, MI355X)",
         "roofline": roofline,
