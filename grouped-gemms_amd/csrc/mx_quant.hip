@@ -10,6 +10,11 @@
 // used for the weight-gradient operands, kernels/backward.py:232-243): a
 // workgroup stages a 32-row x 256-column tile through LDS and each thread
 // quantizes one column block, writing the transposed row of the output.
+//
+// Both-ways kernel (`mxgg_quantize_mx_both`): the same tile also yields the
+// row-wise blocks, so one read of the source gives to_mx(x) and
+// to_mx(x.t().contiguous()): 2 + 2 * (1 + 1/32) = 4.06 bytes per bf16
+// element instead of 6.06 for the two passes.
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
@@ -157,6 +162,87 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint8_t* __restri
   scales[col * ld_s + r0 / 32] = (uint8_t)s;
 }
 
+// Row-wise and column-wise quantization of one 32 x 256 tile of batch
+// blockIdx.z: thread t quantizes the row block (row t / 8, columns
+// 32 (t % 8) .. +31) and the column block (column t, the tile's 32 rows).
+template <int SRC>
+__global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restrict__ src,
+                                                         int64_t rows, int64_t cols,
+                                                         int64_t ld_src_bytes,
+                                                         uint8_t* __restrict__ q_r, int64_t ld_qr,
+                                                         uint8_t* __restrict__ s_r, int64_t ld_sr,
+                                                         uint8_t* __restrict__ q_c, int64_t ld_qc,
+                                                         uint8_t* __restrict__ s_c, int64_t ld_sc) {
+  constexpr int EB = elem_bytes<SRC>();
+  constexpr int TC = 256;
+  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * TC * EB];
+  const int64_t b = blockIdx.z;
+  src += b * rows * ld_src_bytes;
+  q_r += b * rows * ld_qr;
+  s_r += b * rows * ld_sr;
+  q_c += b * cols * ld_qc;
+  s_c += b * cols * ld_sc;
+  const int64_t r0 = (int64_t)blockIdx.y * 32;
+  const int64_t c0 = (int64_t)blockIdx.x * TC;
+  const int t = threadIdx.x;
+  constexpr int CHUNKS_PER_ROW = TC * EB / 16;
+  for (int i = t; i < 32 * CHUNKS_PER_ROW; i += 256) {
+    int rr = i / CHUNKS_PER_ROW;
+    int cc = i - rr * CHUNKS_PER_ROW;
+    int64_t col = c0 + (int64_t)cc * (16 / EB);
+    if (col < cols) {
+      uint4 u = *reinterpret_cast<const uint4*>(src + (r0 + rr) * ld_src_bytes + col * EB);
+      *reinterpret_cast<uint4*>(&tile[(rr * TC) * EB + cc * 16]) = u;
+    }
+  }
+  __syncthreads();
+  auto load = [&](int rr, int cc) -> float {
+    const uint8_t* p = &tile[(rr * TC + cc) * EB];
+    if constexpr (SRC == MXGG_DTYPE_BF16) return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+    else if constexpr (SRC == MXGG_DTYPE_F16) return (float)*reinterpret_cast<const _Float16*>(p);
+    else return *reinterpret_cast<const float*>(p);
+  };
+  auto quant32 = [&](const float (&v)[32], uint8_t* dst, uint8_t* sdst) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      uint32_t a = abs_bits(v[i]);
+      m = a > m ? a : m;
+    }
+    const uint32_t sc = floor_scale(m, 8);
+    const float mul = inv_scale(sc);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      w[i] = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[i] |= e4m3_code(v[4 * i + j], mul) << (8 * j);
+    }
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+    *sdst = (uint8_t)sc;
+  };
+  {
+    const int rr = t / 8, cb = t % 8;
+    const int64_t col0 = c0 + cb * 32;
+    if (col0 < cols) {                             // cols % 32 == 0: whole blocks
+      float v[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) v[i] = load(rr, cb * 32 + i);
+      quant32(v, q_r + (r0 + rr) * ld_qr + col0, s_r + (r0 + rr) * ld_sr + col0 / 32);
+    }
+  }
+  {
+    const int64_t col = c0 + t;
+    if (col < cols) {
+      float v[32];
+#pragma unroll
+      for (int rr = 0; rr < 32; ++rr) v[rr] = load(rr, t);
+      quant32(v, q_c + col * ld_qc + r0, s_c + col * ld_sc + r0 / 32);
+    }
+  }
+}
+
 }  // namespace mxgg
 
 using namespace mxgg;
@@ -236,4 +322,41 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
   else
     hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F32>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, scales, ld_s);
   return launch_status("quantize_mx_dim0");
+}
+
+extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
+                                     int64_t ld_src, void* q_rows, int64_t ld_qr, uint8_t* s_rows,
+                                     int64_t ld_sr, void* q_cols, int64_t ld_qc, uint8_t* s_cols,
+                                     int64_t ld_sc, void* stream) {
+  clear_error();
+  if (src_dtype != MXGG_DTYPE_BF16 && src_dtype != MXGG_DTYPE_F16 && src_dtype != MXGG_DTYPE_F32)
+    return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: src_dtype %d not one of BF16/F16/F32", src_dtype);
+  if (batch < 0 || rows < 0 || cols < 0) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: negative shape");
+  if (rows % 32 || cols % 32)
+    return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: both dims (%lld, %lld) must be divisible by block_size 32",
+                (long long)rows, (long long)cols);
+  if (ld_src < cols || ld_qr < cols || ld_sr < cols / 32 || ld_qc < rows || ld_sc < rows / 32)
+    return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: row stride smaller than the row");
+  if (batch == 0 || rows == 0 || cols == 0) return MXGG_OK;
+  if (!src || !q_rows || !s_rows || !q_cols || !s_cols)
+    return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: null pointer");
+  const int eb = src_dtype == MXGG_DTYPE_F32 ? 4 : 2;
+  if (((uintptr_t)src % 16) || ((ld_src * eb) % 16))
+    return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: source rows must be 16-byte aligned");
+  if (((uintptr_t)q_rows % 16) || (ld_qr % 16) || ((uintptr_t)q_cols % 16) || (ld_qc % 16))
+    return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: output rows must be 16-byte aligned");
+  if (int rc = require_device()) return rc;
+  dim3 grid((unsigned)((cols + 255) / 256), (unsigned)(rows / 32), (unsigned)batch);
+  if (rows / 32 > 65535 || batch > 65535) return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx_both: too many rows or batches");
+  hipStream_t st = (hipStream_t)stream;
+  const uint8_t* s8 = (const uint8_t*)src;
+  const int64_t lsb = ld_src * eb;
+#define MXGG_QBOTH(SRC)                                                                                  \
+  hipLaunchKernelGGL(quant_both_kernel<SRC>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q_rows, \
+                     ld_qr, s_rows, ld_sr, (uint8_t*)q_cols, ld_qc, s_cols, ld_sc)
+  if (src_dtype == MXGG_DTYPE_BF16) MXGG_QBOTH(MXGG_DTYPE_BF16);
+  else if (src_dtype == MXGG_DTYPE_F16) MXGG_QBOTH(MXGG_DTYPE_F16);
+  else MXGG_QBOTH(MXGG_DTYPE_F32);
+#undef MXGG_QBOTH
+  return launch_status("quantize_mx_both");
 }

@@ -13,7 +13,8 @@ with eager torch ops in utils.py:67-105).
 from ._common import _rocm_mxfp8_available
 from .backward import triton_mxfp8_wgrad
 from .forward import triton_mxfp8_grouped_mm
-from .quant import to_mx, to_mx_dim0
+from .moe import MXFP8GroupedLinear, mxfp8_grouped_mm
+from .quant import to_mx, to_mx_both, to_mx_dim0
 
 __all__ = [
     "triton_mxfp8_grouped_mm",
@@ -21,4 +22,7 @@ __all__ = [
     "_rocm_mxfp8_available",
     "to_mx",
     "to_mx_dim0",
+    "to_mx_both",
+    "mxfp8_grouped_mm",
+    "MXFP8GroupedLinear",
 ]

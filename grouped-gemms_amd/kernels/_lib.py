@@ -41,6 +41,8 @@ SIGNATURES = {
                                   _c_p, _c_i64, _c_p]),
     "mxgg_quantize_mx_dim0": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64,
                                        _c_p, _c_i64, _c_p]),
+    "mxgg_quantize_mx_both": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,
+                                       _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
     "mxgg_routing_words": (_c_i64, [_c_i32, _c_i64, _c_i32]),
     "mxgg_build_routing": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_p, _c_p]),
     "mxgg_schedule_programs": (_c_i64, [_c_i32, _c_i64, _c_i64, _c_i32, _c_i32]),

@@ -6,6 +6,8 @@ bytes and scales, computed by one fused HIP kernel (``mxgg_quantize_mx``)
 instead of ~10 eager torch kernels.  ``to_mx_dim0`` produces
 ``to_mx(x.t().contiguous())`` in one pass (``mxgg_quantize_mx_dim0``), the
 "dim1-quantized" layout the weight gradient takes (kernels/backward.py:232).
+``to_mx_both`` gives both layouts from one read of the source
+(``mxgg_quantize_mx_both``), for the backward pass of an MoE layer.
 """
 
 from __future__ import annotations
@@ -87,3 +89,38 @@ def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
                                    _stream_handle(data.device))
     _lib.check(rc)
     return s, q.view(torch.float8_e4m3fn)
+
+
+def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32):
+    """``(to_mx(data), to_mx(data.transpose(-2, -1).contiguous()))`` in one pass.
+
+    ``data`` is ``(R, C)`` or ``(B, R, C)`` with ``R`` and ``C`` multiples of
+    32.  Returns ``((scales (.., R, C//32), data (.., R, C)),
+    (scales (.., C, R//32), data (.., C, R)))``, e4m3, bit-identical to the
+    two separate calls.
+    """
+    assert elem_dtype is torch.float8_e4m3fn, "to_mx_both supports e4m3fn only"
+    assert block_size == 32, "block_size must be 32 (OCP MX)"
+    assert data.dim() in (2, 3), "to_mx_both expects a 2-D or 3-D tensor"
+    _require(data, "data")
+    code = _src_code(data)
+    x = data if data.dim() == 3 else data.unsqueeze(0)
+    B, R, C = x.shape
+    assert R % block_size == 0 and C % block_size == 0, (
+        f"both dims ({R}, {C}) must be divisible by block_size {block_size}")
+    x = x.contiguous()
+    if (C * x.element_size()) % 16:
+        raise ValueError(f"to_mx_both needs the last dim ({C}) to span a multiple of 16 bytes")
+    dev = data.device
+    q_r = torch.empty((B, R, C), dtype=torch.uint8, device=dev)
+    s_r = torch.empty((B, R, C // 32), dtype=torch.uint8, device=dev)
+    q_c = torch.empty((B, C, R), dtype=torch.uint8, device=dev)
+    s_c = torch.empty((B, C, R // 32), dtype=torch.uint8, device=dev)
+    lib = _lib.load()
+    rc = lib.mxgg_quantize_mx_both(x.data_ptr(), code, B, R, C, C, q_r.data_ptr(), C, s_r.data_ptr(), C // 32,
+                                   q_c.data_ptr(), R, s_c.data_ptr(), R // 32, _stream_handle(dev))
+    _lib.check(rc)
+    q_r, q_c = q_r.view(torch.float8_e4m3fn), q_c.view(torch.float8_e4m3fn)
+    if data.dim() == 2:
+        return (s_r[0], q_r[0]), (s_c[0], q_c[0])
+    return (s_r, q_r), (s_c, q_c)

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_VERSION 2001 /* major*1000 + minor */
+#define MXGG_VERSION 2002 /* major*1000 + minor */
 
 /* status codes */
 #define MXGG_OK 0
@@ -85,6 +85,24 @@ int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
 int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t cols,
                           int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
                           uint8_t* scales, int64_t ld_s, void* stream);
+
+/*
+ * Both MX layouts from one read of src: q_rows / s_rows = to_mx(src) and
+ * q_cols / s_cols = to_mx(src.t().contiguous()), e4m3, for `batch` stacked
+ * (rows, cols) matrices (batch stride rows * ld_src elements; outputs stacked
+ * the same way).  The fused cast-transpose step the reference's callers need
+ * for the backward pass: a gradient quantized along N for dgrad and along M
+ * for wgrad (kernels/backward.py:232-233), or an expert weight (E, N, K)
+ * quantized along K for the forward and along N, transposed to (E, K, N),
+ * for dgrad (kernels/forward.py:485-488).  Bit-identical to mxgg_quantize_mx
+ * + mxgg_quantize_mx_dim0.
+ *   src     (batch, rows, cols) of src_dtype, row stride ld_src; rows % 32 == 0, cols % 32 == 0
+ *   q_rows  (batch, rows, cols) e4m3, row stride ld_qr;  s_rows (batch, rows, cols/32), row stride ld_sr
+ *   q_cols  (batch, cols, rows) e4m3, row stride ld_qc;  s_cols (batch, cols, rows/32), row stride ld_sc
+ */
+int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
+                          int64_t ld_src, void* q_rows, int64_t ld_qr, uint8_t* s_rows, int64_t ld_sr,
+                          void* q_cols, int64_t ld_qc, uint8_t* s_cols, int64_t ld_sc, void* stream);
 
 /*
  * Routing table of the grouped GEMM, in the reference's buffer format

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.mxgg_version() == 2001
+    assert lib.mxgg_version() == 2002
     assert isinstance(lib.mxgg_last_error_string(), bytes)
 
 
@@ -137,6 +137,14 @@ def test_wgrad_and_quant_validation_without_gpu():
     assert rc == _lib.ERR_UNSUPPORTED
     # empty problems are valid no-ops that never reach the device
     assert lib.mxgg_quantize_mx(None, 0, 0, 64, 64, 0, None, 64, None, 2, None) == 0
+    # both-ways quantizer: both dims must be multiples of 32, strides cover the rows
+    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 40, 64, 64, 16, 64, 16, 2, 16, 40, 16, 1, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"divisible by block_size 32" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 64, 64, 64, 16, 64, 16, 2, 16, 32, 16, 2, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"stride" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_quantize_mx_both(16, 7, 1, 64, 64, 64, 16, 64, 16, 2, 16, 64, 16, 2, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    assert lib.mxgg_quantize_mx_both(None, 0, 0, 64, 64, 64, None, 64, None, 2, None, 64, None, 2, None) == 0
 
 
 def test_import_surface_matches_reference():
@@ -188,6 +196,13 @@ def test_cpu_tensors_fail_loudly():
         triton_mxfp8_grouped_mm(a, b, sa, sb, torch.tensor([64], dtype=torch.int32))
     with pytest.raises(TypeError):
         to_mx(torch.zeros((4, 64), dtype=torch.bfloat16))
+    from kernels import to_mx_both
+    from kernels.moe import mxfp8_grouped_mm
+    with pytest.raises(TypeError):
+        to_mx_both(torch.zeros((64, 64), dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        mxfp8_grouped_mm(torch.zeros((64, 64), dtype=torch.bfloat16), torch.zeros((1, 64, 64), dtype=torch.bfloat16),
+                         torch.tensor([64], dtype=torch.int32))
 
 
 def test_shape_errors_match_reference_types():
