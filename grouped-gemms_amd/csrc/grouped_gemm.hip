@@ -3,6 +3,8 @@
 //   * weight gradient:  out[g]   = GO[:, s:e] @ IA[:, s:e]^T (kernels/backward.py:31-215)
 //   * routing table and tile schedule exposed for testing   (kernels/forward.py:31-51, 296-365)
 //   * scale re-layout feeding both GEMMs                    (the role of kernels/forward.py:367-397)
+//   * split of an under-filled last round along the reduction, with fp32
+//     partial tiles and a reduce kernel        (generalises kernels/backward.py:106-215)
 //
 // Both GEMMs are "NT" products whose two operands are contiguous along the
 // reduction dimension, so they share one main loop:
@@ -51,21 +53,22 @@ constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
 // split: after more rounds the whole tiles finish at spread-out times, the
 // last round's tiles start early, and little idle time is left to recover
 // (measured: a loss from 5 full rounds on).  S is picked by a cost model
-// (microseconds, MI355X kernel traces): the last round of n steps costs about
-// kTailShare * n * kStepUs; cut into S pieces it costs n / S of that, plus
-// kSplitFixedUs (piece prologue and epilogue, two launches) plus the partial
-// traffic, rem * S tiles written and read back (kSplitUsPerMiB).  No split
-// unless that saves at least kSplitMinGainUs (the model is coarse);
-// reductions shorter than kMinSplitTotal steps are never split.
+// (nanoseconds, MI355X kernel traces): the last round of n steps costs about
+// kTailNsPerStep * n (0.75 of 1.7 us per step); cut into S pieces it costs
+// n / S of that, plus kSplitFixedNs (piece prologue and epilogue, two
+// launches) plus the partial traffic, rem * S tiles written and read back
+// (kSplitNsPerMiB).  No split unless that saves at least kSplitMinGainNs (the
+// model is coarse); reductions shorter than kMinSplitTotal steps are never
+// split.  Integer arithmetic: every kernel that recomputes the plan on the
+// device gets the same answer, bit for bit.
 constexpr int kMinSplitSteps = 4;
 constexpr int kMaxSplit = 8;
 constexpr int kMinSplitTotal = 32;
 constexpr int kSplitMaxRounds = 2;
-constexpr float kTailShare = 0.75f;
-constexpr float kStepUs = 1.7f;
-constexpr float kSplitFixedUs = 12.f;
-constexpr float kSplitUsPerMiB = 0.55f;
-constexpr float kSplitMinGainUs = 16.f;
+constexpr int64_t kTailNsPerStep = 1275;
+constexpr int64_t kSplitFixedNs = 12000;
+constexpr int64_t kSplitNsPerMiB = 550;
+constexpr int64_t kSplitMinGainNs = 16000;
 constexpr size_t kSplitBytes = (size_t)64 << 20;   // partial-tile area of a full workspace
 
 struct Split {
@@ -83,11 +86,10 @@ __host__ __device__ inline Split split_plan(int T, int P, int nsteps, int slots,
   if (smax > kMaxSplit) smax = kMaxSplit;
   if (smax > nsteps / kMinSplitSteps) smax = nsteps / kMinSplitSteps;
   if (smax > slots / rem) smax = slots / rem;
-  const float tail = kTailShare * (float)nsteps * kStepUs;
-  float best = kSplitMinGainUs;
+  const int64_t tail = kTailNsPerStep * nsteps;
+  int64_t best = kSplitMinGainNs;
   for (int S = 2; S <= smax; ++S) {
-    const float gain = tail * (1.f - 1.f / (float)S) - kSplitFixedUs -
-                       (float)(rem * S) * (float)tile_kib * (kSplitUsPerMiB / 1024.f);
+    const int64_t gain = tail - tail / S - kSplitFixedNs - (int64_t)rem * S * tile_kib * kSplitNsPerMiB / 1024;
     if (gain > best) {
       best = gain;
       sp.S = S;
@@ -177,8 +179,9 @@ struct Frags {
 // (q = wave*Q + i; R = 16 rows of 64 bytes, or 32 rows of 32 bytes for packed
 // e2m1 W); the lane's row inside a copy and its swizzled chunk do not depend
 // on i, so one per-lane offset serves all copies and the row step of copy i
-// travels in the scalar offset.  The chunk index rides in bits 28..31
-// (offsets stay below 2**26: row strides below 2**23).
+// travels in the scalar offset.  The chunk index rides in bits 28..31 (a
+// lane's offset is at most 31 rows of a stride below 2**23 plus 48 bytes:
+// below 2**28).
 // Scale copy of wave w (w < NSD): slot dwords 256 w .. 256 w + 255, 4 per
 // lane; lane l covers step u and tile row v of the group, at workspace byte
 // s_base + t * s_step for step t of the reduction.
