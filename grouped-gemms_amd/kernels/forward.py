@@ -3,9 +3,11 @@
 Drop-in for kernels/forward.py:461-606 of the reference: same name,
 positional order, defaults and return value.  ``output[s:e] = A[s:e] @ B[g]^T``
 per expert group, MX scales per 32 elements of K, fp32 accumulation, one
-rounding to ``out_dtype``.  The work runs in the hand-written HIP kernel of
-libmxgg (``mxgg_grouped_mm``), which builds the expert->tile routing inside
-the kernel from ``group_end_offsets`` (no host sync, no extra launch).
+rounding to ``out_dtype``.  The work runs in the hand-written HIP kernels of
+libmxgg (``mxgg_grouped_mm``): a scale re-layout launch, then the GEMM, which
+builds the expert->tile routing inside the kernel from ``group_end_offsets``
+(no host sync), and, when the last round of tiles is split along K, the
+piece and reduce launches.
 
 Beyond the reference, the weight may be MXFP4: ``weight`` of dtype
 ``torch.float4_e2m1fn_x2`` (or uint8) with last dim K/2, two e2m1 values per
@@ -119,7 +121,9 @@ def triton_mxfp8_grouped_mm(
     out = torch.empty((M, N), dtype=out_dtype, device=dev)
     code = _out_code(out_dtype)
     lib = _lib.load()
-    # scratch for the scales re-laid step-major (overwritten by the call)
+    # scratch for the scales re-laid step-major and the fp32 partial tiles of a
+    # split last round (overwritten by the call; torch's caching allocator
+    # makes the per-call allocation cheap)
     ws_bytes = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_grouped_mm(
