@@ -176,6 +176,26 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
     return "\n".join(out)
 
 
+def counter_summary(csv_path: str) -> str:
+    """Per-kernel mean of every counter in a ``rocprofv3 --pmc`` counter CSV
+    (GEMM kernels only), e.g. MfmaUtil / LdsBankConflict over a bench run."""
+    import csv
+    acc = {}
+    for r in csv.DictReader(open(csv_path)):
+        n = r["Kernel_Name"].replace("void ", "").split("(")[0]
+        if "mxgg::" not in n or "quant" in n:
+            continue
+        a = acc.setdefault(n, {}).setdefault(r["Counter_Name"], [0.0, 0])
+        a[0] += float(r["Counter_Value"])
+        a[1] += 1
+    names = sorted({c for v in acc.values() for c in v})
+    out = [f"{'kernel':62s} " + " ".join(f"{c:>16s}" for c in names) + f" {'dispatches':>10s}"]
+    for n, v in sorted(acc.items()):
+        cells = " ".join(f"{v[c][0] / v[c][1]:16.4f}" if c in v else f"{'-':>16s}" for c in names)
+        out.append(f"{n[:62]:62s} {cells} {max(x[1] for x in v.values()):10d}")
+    return "\n".join(out)
+
+
 def stats_summary(stats_csv: str, bench_json: str) -> str:
     """Per-kernel table of a ``rocprofv3 --kernel-trace --stats`` run over the
     default bench (its ``*_kernel_stats.csv``), followed by the same run's own
@@ -246,8 +266,8 @@ def cpu_baseline(budget_s: float):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30, help="timed reps per shape")
-    ap.add_argument("--warmup", type=int, default=10, help="untimed reps per shape")
+    ap.add_argument("--steps", type=int, default=60, help="timed reps per shape")
+    ap.add_argument("--warmup", type=int, default=20, help="untimed reps per shape")
     ap.add_argument("--only", choices=("all", "fwd", "dgrad", "wgrad"), default="all")
     ap.add_argument("--shapes", type=int, default=36, help="first N shapes of the sweep")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
@@ -260,10 +280,15 @@ def main():
                     help="summarize two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of "
                          "`bench.py --steps S --warmup W --no-cpu --copy-calibration` (same S, W, --shapes) "
                          "and exit; runs on the CPU")
+    ap.add_argument("--counter-summary", metavar="COUNTER_CSV",
+                    help="per-kernel means of a rocprofv3 --pmc counter CSV and exit; runs on the CPU")
     ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "BENCH_JSON"),
                     help="summarize a rocprofv3 --kernel-trace --stats run of the default bench "
                          "(its kernel_stats.csv and the JSON line it printed) and exit; runs on the CPU")
     args = ap.parse_args()
+    if args.counter_summary:
+        print(counter_summary(args.counter_summary))
+        return
     if args.stats_summary:
         print(stats_summary(*args.stats_summary))
         return
