@@ -755,13 +755,14 @@ struct FwdTile {
 };
 
 // Tile of logical index lt (0 <= lt < tiles) after the XCD swizzle and the
-// GROUP_M band order; false when it holds no output rows.  Wave-uniform.
+// expert-aligned band order (route_tile: bands of at most GROUP_M m-blocks
+// inside one group); false when it holds no output rows.  Wave-uniform.
 template <class C>
 __device__ __forceinline__ bool fwd_tile(const FwdParams& p, int lt, int tiles, int total_m, FwdTile& tl) {
+  (void)total_m;
   const int t = p.xcd > 1 ? xcd_swizzle(lt, tiles, p.xcd) : lt;
-  int pm, pn;
-  pid_grid(t, total_m, p.grid_n, p.group_m, pm, pn);
-  const TileRoute r = route_find(p.offs, p.E, C::BM, pm);
+  int pn;
+  const TileRoute r = route_tile(p.offs, p.E, C::BM, p.grid_n, p.group_m, t, pn);
   if (r.expert < 0) return false;
   tl.expert = r.expert;
   tl.row0 = (int64_t)r.start + (int64_t)r.block * C::BM;
@@ -1084,13 +1085,14 @@ struct FwdChoice {
   int bm, bn, group_m, xcd;
 };
 
-// 256 x 256 tiles with GROUP_M 8 and the 8-XCD swizzle (best on every sweep
-// shape measured, the 2048 x 2048 ones included); 128 x 128 tiles for e4m3
+// 256 x 256 tiles, the 8-XCD swizzle and expert-aligned bands of at most 12
+// m-blocks (route_tile; 12 beat 8 and 16 on the sweep's jagged groups, and
+// the 256 x 256 tile beats 128 x 128 even at N = K = 2048); 128 x 128 tiles for e4m3
 // problems too small to fill half the chip with 256 x 256 tiles and too
 // short (K < 4096) for the split of the last round to make up for it.
 FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, int bn, int gm,
                    int xcd) {
-  FwdChoice c{256, 256, 8, 8};
+  FwdChoice c{256, 256, 12, 8};
   if (b_fmt == MXGG_FMT_E4M3 && K < 4096 && (cdiv(M, 256) + E - 1) * cdiv(N, 256) < 128) {
     c.bm = 128;
     c.bn = 128;

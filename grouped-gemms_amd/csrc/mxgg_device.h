@@ -220,6 +220,61 @@ __device__ __forceinline__ TileRoute route_find(const int32_t* __restrict__ offs
   return r;
 }
 
+// Expert-aligned tile order used by the GEMMs: the tiles of group e (its
+// cdiv(hist[e], BM) m-blocks x grid_n column tiles) are contiguous in the
+// logical order, groups in order; inside a group the m-blocks form bands of
+// at most group_m (balanced: nbands = cdiv(blocks, group_m), height
+// cdiv(blocks, nbands), the last band shorter), column-major inside a band.
+// Unlike the reference's GROUP_M bands over the global m-block index
+// (kernels/forward.py:38-51, `pid_grid` below), no band mixes two groups, so
+// the tiles in flight on an XCD read one group's weights.  Returns the owner
+// of logical tile t (0 <= t < total blocks x grid_n) and its column tile pn;
+// expert < 0 past the end.  Wave-uniform.
+__device__ __forceinline__ TileRoute route_tile(const int32_t* __restrict__ offs, int E, int BM, int grid_n,
+                                                int group_m, int t, int& pn) {
+  const int lane = threadIdx.x & (kWave - 1);
+  TileRoute r{-1, 0, 0, 0};
+  pn = 0;
+  int carry = 0;
+  for (int base = 0; base < E; base += kWave) {
+    int e = base + lane;
+    int nb = 0, h = 0, prev = 0;
+    if (e < E) {
+      int end = offs[e];
+      prev = e > 0 ? offs[e - 1] : 0;
+      h = end - prev;
+      nb = h > 0 ? (h + BM - 1) / BM : 0;
+    }
+    const int nt = nb * grid_n;
+    int incl = wave_incl_scan(nt) + carry;
+    int excl = incl - nt;
+    bool own = (e < E) && (nt > 0) && (t >= excl) && (t < incl);
+    unsigned long long m = __ballot(own);
+    if (m) {
+      int src = __ffsll((long long)m) - 1;
+      const int local = t - uniform(__shfl(excl, src, kWave));
+      const int blocks = uniform(__shfl(nb, src, kWave));
+      const int hh = uniform(__shfl(h, src, kWave));
+      const int g = group_m > 0 ? group_m : 1;
+      const int nbands = (blocks + g - 1) / g;
+      const int bh = (blocks + nbands - 1) / nbands;           // band height
+      int b = local / (bh * grid_n);
+      if (b > nbands - 1) b = nbands - 1;
+      const int in_band = local - b * bh * grid_n;
+      const int hb = b == nbands - 1 ? blocks - b * bh : bh;   // this band's height
+      r.expert = uniform(base + src);
+      r.block = b * bh + in_band % hb;
+      r.start = uniform(__shfl(prev, src, kWave));
+      const int rem = hh - r.block * BM;
+      r.rows = rem < BM ? rem : BM;
+      pn = in_band / hb;
+      return r;
+    }
+    carry = uniform(__shfl(incl, kWave - 1, kWave));
+  }
+  return r;
+}
+
 // XCD swizzle (kernels/forward.py:31-36): program ids are dispatched round-robin
 // to X XCDs; give every XCD a contiguous range of the logical tile order.
 __device__ __forceinline__ int xcd_swizzle(int pid, int domain, int X) {
