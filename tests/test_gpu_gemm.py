@@ -133,6 +133,21 @@ def test_fwd_out_dtypes(gpu, out_dtype):
     assert err <= (1e-4 if out_dtype == torch.float32 else 1e-3), err
 
 
+@pytest.mark.parametrize("gm", [3, 12])
+def test_fwd_many_groups(gpu, gm):
+    """80 groups, a fifth of them empty, sizes 0..96 rows: the in-kernel tile
+    order (groups contiguous, bands of at most GROUP_M m-blocks inside a
+    group) scans the groups in two 64-lane passes; every tile must be
+    computed exactly once."""
+    E, M, N, K = 80, 8192, 384, 256
+    rng = np.random.default_rng(80 + gm)
+    sizes = rng.integers(1, 4, size=E) * 32
+    sizes[rng.choice(E, 16, replace=False)] = 0
+    offs = [int(v) for v in np.cumsum(sizes)]
+    out, ref, hp = _fwd_case(E, M, N, K, offs, gpu, seed=gm, std_b=1.0, GROUP_M=gm)
+    _assert_close(out, ref, hp, rows=offs[-1])
+
+
 def test_fwd_group_m_xcd_options(gpu):
     E, M, N, K = 3, 1536, 1024, 256
     offs = [512, 1024, 1536]
