@@ -585,10 +585,11 @@ constexpr int store_pass_rows(int fm, int lim) {
   return best;
 }
 
-template <class C>
+// BF16: the 16-bit output type (bf16, else f16), fixed at compile time so the
+// staging loop carries no per-write type test.
+template <class C, bool BF16>
 __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], uint8_t* smem,
-                                               uint8_t* out, int64_t ldo, int rows, int cols,
-                                               int out_dtype) {
+                                               uint8_t* out, int64_t ldo, int rows, int cols) {
   constexpr int RB = C::WTN * 2;                 // staged row bytes
   constexpr int NCH = RB / 16;                   // 16-byte chunks per row
   constexpr int AVAIL = C::LDS / C::NW;           // LDS bytes per wave
@@ -599,6 +600,8 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], 
   const int lane = threadIdx.x % kWave;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
   uint8_t* area = smem + wave * (FPP * 32 * RB);
+  // a wave's rows and columns all inside the output: no per-store checks
+  const bool whole = (wm + 1) * C::WTM <= rows && (wn + 1) * C::WTN <= cols;
 #pragma unroll
   for (int i0 = 0; i0 < C::FM; i0 += FPP) {
     __syncthreads();
@@ -611,7 +614,7 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], 
         for (int q4 = 0; q4 < 4; ++q4) {
           const v16f& a = acc[i0 + ii][j];
           uint32_t w0, w1;
-          if (out_dtype == MXGG_DTYPE_BF16) {
+          if constexpr (BF16) {
             w0 = pack_bf16x2(a[4 * q4 + 0], a[4 * q4 + 1]);
             w1 = pack_bf16x2(a[4 * q4 + 2], a[4 * q4 + 3]);
           } else {
@@ -629,22 +632,34 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], 
     }
     __syncthreads();
     constexpr int RPI = 64 / NCH;                        // rows per read instruction
+    if (whole) {
 #pragma unroll
-    for (int it = 0; it < FPP * 32 / RPI; ++it) {
-      const int r = it * RPI + lane / NCH;
-      const int c = lane % NCH;
-      const uint4 v = *reinterpret_cast<const uint4*>(area + r * RB + ((c ^ (r % NCH)) * 16));
-      const int row = wm * C::WTM + i0 * 32 + r;
-      const int col = wn * C::WTN + c * 8;
-      if (row < rows) {
-        uint16_t* p = reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + col;
-        if (col + 8 <= cols) {
-          *reinterpret_cast<uint4*>(p) = v;
-        } else {
-          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      for (int it = 0; it < FPP * 32 / RPI; ++it) {
+        const int r = it * RPI + lane / NCH;
+        const int c = lane % NCH;
+        const uint4 v = *reinterpret_cast<const uint4*>(area + r * RB + ((c ^ (r % NCH)) * 16));
+        const int row = wm * C::WTM + i0 * 32 + r;
+        const int col = wn * C::WTN + c * 8;
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + col) = v;
+      }
+    } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (col + e < cols) p[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+      for (int it = 0; it < FPP * 32 / RPI; ++it) {
+        const int r = it * RPI + lane / NCH;
+        const int c = lane % NCH;
+        const uint4 v = *reinterpret_cast<const uint4*>(area + r * RB + ((c ^ (r % NCH)) * 16));
+        const int row = wm * C::WTM + i0 * 32 + r;
+        const int col = wn * C::WTN + c * 8;
+        if (row < rows) {
+          uint16_t* p = reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + col;
+          if (col + 8 <= cols) {
+            *reinterpret_cast<uint4*>(p) = v;
+          } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (col + e < cols) p[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+          }
         }
       }
     }
@@ -819,7 +834,8 @@ __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int l
     const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
     uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
     if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
-      store_tile_lds<C>(acc, smem, o, p.ldo, rows, cols, p.out_dtype);
+      p.out_dtype == MXGG_DTYPE_BF16 ? store_tile_lds<C, true>(acc, smem, o, p.ldo, rows, cols)
+                                     : store_tile_lds<C, false>(acc, smem, o, p.ldo, rows, cols);
     else
       store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
   }
@@ -1000,7 +1016,7 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
   if (esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
-    store_tile_lds<C>(acc, smem, o, p.K, rows, cols, p.out_dtype);
+    store_tile_lds<C, true>(acc, smem, o, p.K, rows, cols);   // wgrad: bf16 or f32 only
   else
     store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
 }
