@@ -772,12 +772,14 @@ struct FwdTile {
 // Tile of logical index lt (0 <= lt < tiles) after the XCD swizzle and the
 // expert-aligned band order (route_tile: bands of at most GROUP_M m-blocks
 // inside one group); false when it holds no output rows.  Wave-uniform.
+// wg: the groups as load_groups read them when E <= 64 (else offs is read).
 template <class C>
-__device__ __forceinline__ bool fwd_tile(const FwdParams& p, int lt, int tiles, int total_m, FwdTile& tl) {
-  (void)total_m;
+__device__ __forceinline__ bool fwd_tile(const FwdParams& p, int lt, int tiles, const WaveGroups& wg,
+                                         FwdTile& tl) {
   const int t = p.xcd > 1 ? xcd_swizzle(lt, tiles, p.xcd) : lt;
   int pn;
-  const TileRoute r = route_tile(p.offs, p.E, C::BM, p.grid_n, p.group_m, t, pn);
+  const TileRoute r = p.E <= kWave ? route_tile(wg, p.E, C::BM, p.grid_n, p.group_m, t, pn)
+                                   : route_tile(p.offs, p.E, C::BM, p.grid_n, p.group_m, t, pn);
   if (r.expert < 0) return false;
   tl.expert = r.expert;
   tl.row0 = (int64_t)r.start + (int64_t)r.block * C::BM;
@@ -799,9 +801,9 @@ __device__ __forceinline__ Split fwd_split(const FwdParams& p, int tiles) {
 // slot `slot` (PIECES = true).
 template <class C, bool PIECES>
 __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int lt, int piece, int S, int slot,
-                                        int tiles, int total_m) {
+                                        int tiles, const WaveGroups& wg) {
   FwdTile tl;
-  if (!fwd_tile<C>(p, lt, tiles, total_m, tl)) return;
+  if (!fwd_tile<C>(p, lt, tiles, wg, tl)) return;
   const int64_t row0 = tl.row0, n0 = tl.n0;
   const int rows = tl.rows, cols = tl.cols;
 
@@ -841,6 +843,18 @@ __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int l
   }
 }
 
+// Groups of a forward launch and its m-block count: one read of offs when
+// E <= 64 (kept for the tile lookup), else a scan of offs in 64-group chunks.
+template <class C>
+__device__ __forceinline__ int fwd_groups(const FwdParams& p, WaveGroups& wg) {
+  if (p.E <= kWave) {
+    wg = load_groups(p.offs, p.E, C::BM);
+    return wg.total;
+  }
+  wg = WaveGroups{0, 0, 0, 0, 0};
+  return route_total(p.offs, p.E, C::BM);
+}
+
 // PIECES = false: workgroup i < dp computes tile i whole.  PIECES = true:
 // workgroup u < units computes piece u % S of tile dp + u / S into partial
 // slot u.  Other workgroups exit.  (Two kernels rather than one with both
@@ -848,14 +862,14 @@ __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int l
 template <class C, bool PIECES>
 __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
-  const int total_m = route_total(p.offs, p.E, C::BM);
-  const int tiles = total_m * p.grid_n;
+  WaveGroups wg;
+  const int tiles = fwd_groups<C>(p, wg) * p.grid_n;
   const Split sp = fwd_split<C>(p, tiles);
   const int pid = blockIdx.x;
   if constexpr (PIECES) {
-    if (pid < sp.units) fwd_run<C, true>(p, smem, sp.dp + pid / sp.S, pid % sp.S, sp.S, pid, tiles, total_m);
+    if (pid < sp.units) fwd_run<C, true>(p, smem, sp.dp + pid / sp.S, pid % sp.S, sp.S, pid, tiles, wg);
   } else {
-    if (pid < sp.dp) fwd_run<C, false>(p, smem, pid, 0, 1, 0, tiles, total_m);
+    if (pid < sp.dp) fwd_run<C, false>(p, smem, pid, 0, 1, 0, tiles, wg);
   }
 }
 
@@ -907,8 +921,8 @@ struct ReduceShape {
 // offs exactly as fwd_kernel computed it.
 template <class C>
 __global__ __launch_bounds__(256) void fwd_reduce_kernel(FwdParams p) {
-  const int total_m = route_total(p.offs, p.E, C::BM);
-  const int tiles = total_m * p.grid_n;
+  WaveGroups wg;
+  const int tiles = fwd_groups<C>(p, wg) * p.grid_n;
   const Split sp = fwd_split<C>(p, tiles);
   if (sp.units == 0) return;
   constexpr int CH = ReduceShape<C>::CH;
@@ -918,7 +932,7 @@ __global__ __launch_bounds__(256) void fwd_reduce_kernel(FwdParams p) {
   for (int item = blockIdx.x; item < rem * CH; item += gridDim.x) {
     const int v = item / CH, f = (item % CH) * 4 + wave_id();
     FwdTile tl;
-    if (!fwd_tile<C>(p, sp.dp + v, tiles, total_m, tl)) continue;
+    if (!fwd_tile<C>(p, sp.dp + v, tiles, wg, tl)) continue;
     float acc[16];
     sum_pieces<C>(p.part + (int64_t)v * sp.S * (C::BM * C::BN), sp.S, f, lane, acc);
     store_fragment_lane<C, false>(acc, f, lane, p.out + (tl.row0 * p.ldo + tl.n0) * esz, p.ldo, tl.rows,

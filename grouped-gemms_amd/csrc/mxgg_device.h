@@ -143,15 +143,23 @@ constexpr uint32_t kOOB = 0x80000000u;  // voffset that is always out of range
 // wave-level scans
 // ---------------------------------------------------------------------------
 
+// Inclusive prefix sum over the 64 lanes of a wave in DPP steps (no LDS):
+// Hillis-Steele shifts by 1, 2, 4, 8 inside each 16-lane row, then the last
+// lane of rows 0 and 2 is added to rows 1 and 3 (row_bcast:15) and lane 31 to
+// rows 2 and 3 (row_bcast:31).  Sources outside the row, and rows the mask
+// leaves out, contribute the `old` operand, 0.
 __device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    int u = __shfl_up(v, d, kWave);
-    if (lane >= d) v += u;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31 into rows 2, 3
   return v;
 }
+
+// Value of v in lane `src` (wave-uniform src), as a scalar.
+__device__ __forceinline__ int lane_value(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
 
 // ---------------------------------------------------------------------------
 // routing (kernels/forward.py:296-365 semantics)
@@ -173,7 +181,7 @@ __device__ __forceinline__ int route_total(const int32_t* __restrict__ offs, int
       nb = h > 0 ? (h + BM - 1) / BM : 0;
     }
     int incl = wave_incl_scan(nb);
-    carry += uniform(__shfl(incl, kWave - 1, kWave));
+    carry += lane_value(incl, kWave - 1);
   }
   return carry;
 }
@@ -206,16 +214,16 @@ __device__ __forceinline__ TileRoute route_find(const int32_t* __restrict__ offs
     unsigned long long m = __ballot(own);
     if (m) {
       int src = __ffsll((long long)m) - 1;
-      int ex = uniform(__shfl(excl, src, kWave));
+      int ex = lane_value(excl, src);
       r.expert = uniform(base + src);
       r.block = pid_m - ex;
-      r.start = uniform(__shfl(prev, src, kWave));
-      int hh = uniform(__shfl(h, src, kWave));
+      r.start = lane_value(prev, src);
+      int hh = lane_value(h, src);
       int rem = hh - r.block * BM;
       r.rows = rem < BM ? rem : BM;
       return r;
     }
-    carry = uniform(__shfl(incl, kWave - 1, kWave));
+    carry = lane_value(incl, kWave - 1);
   }
   return r;
 }
@@ -230,6 +238,38 @@ __device__ __forceinline__ TileRoute route_find(const int32_t* __restrict__ offs
 // the tiles in flight on an XCD read one group's weights.  Returns the owner
 // of logical tile t (0 <= t < total blocks x grid_n) and its column tile pn;
 // expert < 0 past the end.  Wave-uniform.
+// One 64-group chunk of the lookup: lane l holds group base + l (first row
+// prev, rows h, blocks nb) and incl, the inclusive scan of nb over all groups
+// up to it.  True, with r and pn filled, when a lane of the chunk owns t.
+__device__ __forceinline__ bool route_tile_chunk(int base, int E, int BM, int grid_n, int group_m, int t,
+                                                 int prev, int h, int nb, int incl, TileRoute& r, int& pn) {
+  const int e = base + (int)(threadIdx.x & (kWave - 1));
+  const int nt = nb * grid_n;
+  const int tincl = incl * grid_n;
+  const int texcl = tincl - nt;
+  const bool own = (e < E) && (nt > 0) && (t >= texcl) && (t < tincl);
+  const unsigned long long m = __ballot(own);
+  if (!m) return false;
+  const int src = __ffsll((long long)m) - 1;
+  const int local = t - lane_value(texcl, src);
+  const int blocks = lane_value(nb, src);
+  const int hh = lane_value(h, src);
+  const int g = group_m > 0 ? group_m : 1;
+  const int nbands = (blocks + g - 1) / g;
+  const int bh = (blocks + nbands - 1) / nbands;           // band height
+  int b = local / (bh * grid_n);
+  if (b > nbands - 1) b = nbands - 1;
+  const int in_band = local - b * bh * grid_n;
+  const int hb = b == nbands - 1 ? blocks - b * bh : bh;   // this band's height
+  r.expert = uniform(base + src);
+  r.block = b * bh + in_band % hb;
+  r.start = lane_value(prev, src);
+  const int rem = hh - r.block * BM;
+  r.rows = rem < BM ? rem : BM;
+  pn = in_band / hb;
+  return true;
+}
+
 __device__ __forceinline__ TileRoute route_tile(const int32_t* __restrict__ offs, int E, int BM, int grid_n,
                                                 int group_m, int t, int& pn) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -245,33 +285,39 @@ __device__ __forceinline__ TileRoute route_tile(const int32_t* __restrict__ offs
       h = end - prev;
       nb = h > 0 ? (h + BM - 1) / BM : 0;
     }
-    const int nt = nb * grid_n;
-    int incl = wave_incl_scan(nt) + carry;
-    int excl = incl - nt;
-    bool own = (e < E) && (nt > 0) && (t >= excl) && (t < incl);
-    unsigned long long m = __ballot(own);
-    if (m) {
-      int src = __ffsll((long long)m) - 1;
-      const int local = t - uniform(__shfl(excl, src, kWave));
-      const int blocks = uniform(__shfl(nb, src, kWave));
-      const int hh = uniform(__shfl(h, src, kWave));
-      const int g = group_m > 0 ? group_m : 1;
-      const int nbands = (blocks + g - 1) / g;
-      const int bh = (blocks + nbands - 1) / nbands;           // band height
-      int b = local / (bh * grid_n);
-      if (b > nbands - 1) b = nbands - 1;
-      const int in_band = local - b * bh * grid_n;
-      const int hb = b == nbands - 1 ? blocks - b * bh : bh;   // this band's height
-      r.expert = uniform(base + src);
-      r.block = b * bh + in_band % hb;
-      r.start = uniform(__shfl(prev, src, kWave));
-      const int rem = hh - r.block * BM;
-      r.rows = rem < BM ? rem : BM;
-      pn = in_band / hb;
-      return r;
-    }
-    carry = uniform(__shfl(incl, kWave - 1, kWave));
+    const int incl = wave_incl_scan(nb) + carry;
+    if (route_tile_chunk(base, E, BM, grid_n, group_m, t, prev, h, nb, incl, r, pn)) return r;
+    carry = lane_value(incl, kWave - 1);
   }
+  return r;
+}
+
+// Groups 0 .. E-1 of a launch with E <= 64, one per lane, read from offs once
+// for both the block count (total) and the tile lookup (route_tile below).
+struct WaveGroups {
+  int prev, h, nb, incl;   // lane e: first row, rows, BM-row blocks, inclusive block scan
+  int total;               // blocks over all groups (wave-uniform)
+};
+
+__device__ __forceinline__ WaveGroups load_groups(const int32_t* __restrict__ offs, int E, int BM) {
+  const int e = threadIdx.x & (kWave - 1);
+  WaveGroups g{0, 0, 0, 0, 0};
+  if (e < E) {
+    const int end = offs[e];
+    g.prev = e > 0 ? offs[e - 1] : 0;
+    g.h = end - g.prev;
+    g.nb = g.h > 0 ? (g.h + BM - 1) / BM : 0;
+  }
+  g.incl = wave_incl_scan(g.nb);
+  g.total = lane_value(g.incl, kWave - 1);
+  return g;
+}
+
+__device__ __forceinline__ TileRoute route_tile(const WaveGroups& wg, int E, int BM, int grid_n, int group_m,
+                                                int t, int& pn) {
+  TileRoute r{-1, 0, 0, 0};
+  pn = 0;
+  route_tile_chunk(0, E, BM, grid_n, group_m, t, wg.prev, wg.h, wg.nb, wg.incl, r, pn);
   return r;
 }
 
