@@ -86,10 +86,15 @@ __host__ __device__ inline Split split_plan(int T, int P, int nsteps, int slots,
   if (smax > kMaxSplit) smax = kMaxSplit;
   if (smax > nsteps / kMinSplitSteps) smax = nsteps / kMinSplitSteps;
   if (smax > slots / rem) smax = slots / rem;
-  const int64_t tail = kTailNsPerStep * nsteps;
-  int64_t best = kSplitMinGainNs;
-  for (int S = 2; S <= smax; ++S) {
-    const int64_t gain = tail - tail / S - kSplitFixedNs - (int64_t)rem * S * tile_kib * kSplitNsPerMiB / 1024;
+  // int32 throughout: tail < 1275 * 2^20, and rem * S <= slots <= 4096 with
+  // tile_kib <= 256 keeps the staging term below 2^30.  Unrolled, every
+  // tail / S has a constant divisor.
+  const int tail = (int)kTailNsPerStep * (nsteps < (1 << 20) ? nsteps : (1 << 20));
+  int best = (int)kSplitMinGainNs;
+#pragma unroll
+  for (int S = 2; S <= kMaxSplit; ++S) {
+    if (S > smax) break;
+    const int gain = tail - tail / S - (int)kSplitFixedNs - rem * S * tile_kib * (int)kSplitNsPerMiB / 1024;
     if (gain > best) {
       best = gain;
       sp.S = S;

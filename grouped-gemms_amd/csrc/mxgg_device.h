@@ -22,6 +22,7 @@ __device__ __forceinline__ int wave_id() {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+
 // ---------------------------------------------------------------------------
 // element conversions (bit-exact with the FLOOR-mode `to_mx`, utils.py:84-105)
 // ---------------------------------------------------------------------------
@@ -261,12 +262,13 @@ __device__ __forceinline__ bool route_tile_chunk(int base, int E, int BM, int gr
   if (b > nbands - 1) b = nbands - 1;
   const int in_band = local - b * bh * grid_n;
   const int hb = b == nbands - 1 ? blocks - b * bh : bh;   // this band's height
+  const int col = in_band / hb;
   r.expert = uniform(base + src);
-  r.block = b * bh + in_band % hb;
+  r.block = b * bh + (in_band - col * hb);
   r.start = lane_value(prev, src);
   const int rem = hh - r.block * BM;
   r.rows = rem < BM ? rem : BM;
-  pn = in_band / hb;
+  pn = col;
   return true;
 }
 
@@ -324,10 +326,11 @@ __device__ __forceinline__ TileRoute route_tile(const WaveGroups& wg, int E, int
 // XCD swizzle (kernels/forward.py:31-36): program ids are dispatched round-robin
 // to X XCDs; give every XCD a contiguous range of the logical tile order.
 __device__ __forceinline__ int xcd_swizzle(int pid, int domain, int X) {
-  int per = domain / X;
-  int extra = domain % X;
-  int g = pid % X;
-  return g * per + (g < extra ? g : extra) + pid / X;
+  const int per = domain / X;
+  const int extra = domain - per * X;
+  const int q = pid / X;
+  const int g = pid - q * X;
+  return g * per + (g < extra ? g : extra) + q;
 }
 
 // GROUP_M band ordering (kernels/forward.py:38-51).
