@@ -1118,20 +1118,43 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct FwdChoice {
   int bm, bn, group_m, xcd;
+  bool split;   // the last round may be split along K (workspace permitting)
 };
 
-// 256 x 256 tiles, the 8-XCD swizzle and expert-aligned bands of at most 12
-// m-blocks (route_tile; 12 beat 8 and 16 on the sweep's jagged groups, and
-// the 256 x 256 tile beats 128 x 128 even at N = K = 2048); 128 x 128 tiles for e4m3
-// problems too small to fill half the chip with 256 x 256 tiles and too
+struct TunedFwd {
+  int E, M, N, K, b_fmt, bm, bn, group_m, xcd, split;
+};
+
+#include "tuned_fwd.h"
+
+// Tuned entry for (E, M, N, K, b_fmt): same E, N, K and format, M within a
+// factor of two of the swept M; null when the sweep did not cover the shape.
+const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
+  for (const TunedFwd* t = kTunedFwd; t->E; ++t)
+    if (t->E == E && t->N == N && t->K == K && t->b_fmt == b_fmt && 2 * M >= t->M && M <= 2 * (int64_t)t->M)
+      return t;
+  return nullptr;
+}
+
+// A tuned entry when the sweep covered the shape.  Otherwise 256 x 256
+// tiles, the 8-XCD swizzle and expert-aligned bands of at most 12 m-blocks
+// (route_tile; 12 beat 8 and 16 on the sweep's jagged groups, and the
+// 256 x 256 tile beats 128 x 128 even at N = K = 2048); 128 x 128 tiles for
+// e4m3 problems too small to fill half the chip with 256 x 256 tiles and too
 // short (K < 4096) for the split of the last round to make up for it.
+// Requests (nonzero bm, bn, gm, xcd) override field by field, and any request
+// leaves the split to the workspace (a tuned "whole tiles only" applies to
+// calls that request nothing).
 FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, int bn, int gm,
                    int xcd) {
-  FwdChoice c{256, 256, 12, 8};
-  if (b_fmt == MXGG_FMT_E4M3 && K < 4096 && (cdiv(M, 256) + E - 1) * cdiv(N, 256) < 128) {
+  FwdChoice c{256, 256, 12, 8, true};
+  if (const TunedFwd* t = find_tuned(E, M, N, K, b_fmt)) {
+    c = FwdChoice{t->bm, t->bn, t->group_m, t->xcd, t->split != 0};
+  } else if (b_fmt == MXGG_FMT_E4M3 && K < 4096 && (cdiv(M, 256) + E - 1) * cdiv(N, 256) < 128) {
     c.bm = 128;
     c.bn = 128;
   }
+  if (bm || bn || gm || xcd) c.split = true;
   if (bm) c.bm = bm;
   if (bn) c.bn = bn;
   if (gm) c.group_m = gm;
@@ -1353,7 +1376,7 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   }
   // partial tiles of a split last round after the scales (optional)
   const size_t part_off = align256(need);
-  float* part = ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
+  float* part = c.split && ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
   const size_t part_bytes = part ? ws_bytes - part_off : 0;
   FwdParams p{A, lda, B, ldb_n, ldb_e, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
               (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0};

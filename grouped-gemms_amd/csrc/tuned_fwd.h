@@ -1,0 +1,19 @@
+// Tuned forward launch configurations, one per swept shape, consulted by
+// pick_fwd (grouped_gemm.hip) before its built-in rule.  Written by
+// `python grouped-gemms_amd/tune_driver.py --emit-header` from the sweep's
+// best.json; regenerate rather than edit.  An entry applies to calls with
+// the same E, N, K and weight format and M within a factor of two of the
+// swept M.  Fields: E, M, N, K, b_fmt (0 e4m3, 4 e2m1), block_m, block_n,
+// group_m, xcd swizzle, split (1: the last round may be split along K when
+// the workspace allows it, 0: whole tiles only).
+// sweep: 36 shapes (e4m3, 5 offset draws), 7 with a gain of at least 2% on every draw; AMD Radeon Graphics
+static const TunedFwd kTunedFwd[] = {
+    {1, 16640, 2048, 2048, 0, 128, 128, 8, 8, 0},   // 105.4 us
+    {1, 16640, 2048, 5120, 0, 256, 256, 8, 1, 1},   // 219.3 us
+    {1, 16640, 2048, 8192, 0, 256, 256, 4, 1, 1},   // 295.2 us
+    {1, 16640, 5120, 2048, 0, 256, 256, 4, 1, 0},   // 204.8 us
+    {1, 16640, 5120, 5120, 0, 256, 256, 8, 8, 1},   // 461.4 us
+    {1, 16640, 5120, 8192, 0, 256, 256, 4, 1, 0},   // 670.8 us
+    {1, 16640, 8192, 2048, 0, 256, 256, 8, 8, 0},   // 308.4 us
+    {0, 0, 0, 0, 0, 0, 0, 0, 0, 0},   // end
+};
