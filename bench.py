@@ -73,10 +73,11 @@ def fwd_kernel_name(cfg: dict) -> str:
     N, B format, LDS stages>, pieces=false.  A call may also launch the piece
     and reduce kernels of a split last round; bench.py's event time covers
     the whole call."""
-    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4>, false>"
+    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4>, false, 1>"
 
 
-WGRAD_KERNEL = "mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4>, false>"
+# whole-tile kernels with the bf16 epilogue (template argument 1): the bench's outputs are bf16 with aligned rows
+WGRAD_KERNEL = "mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4>, false, 1>"
 
 
 def canon(kernel: str) -> str:
@@ -142,7 +143,7 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
         # whole-tile GEMM kernels only: one per call (piece / reduce kernels of a
         # split last round, when launched, are left out of the per-call match)
         scaled[counter] = [(n, v * factor * 1024.0) for _, n, v in rows
-                           if ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and "false>" in n]
+                           if ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n]
     f, w = scaled["FETCH_SIZE"], scaled["WRITE_SIZE"]
     per = warmup + steps
     shapes = SHAPES[:n_shapes]

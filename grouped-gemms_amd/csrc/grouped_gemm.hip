@@ -768,6 +768,15 @@ struct FwdParams {
   float* part; int par; int slots;          // split: partial slots, resident workgroups, slot count
 };
 
+// Epilogue of the whole-tile kernels, fixed at compile time so that the
+// common case carries none of the others' register pressure (with every
+// variant in one kernel the allocator spilled accumulators to scratch and
+// reloaded them serially in the epilogue): kEpiBf16 is a bf16 output whose
+// rows are 16-byte aligned (row stride a multiple of 8 elements, 16-byte
+// aligned base), staged through LDS; kEpiAny takes every output type and
+// alignment.
+constexpr int kEpiAny = 0, kEpiBf16 = 1;
+
 struct FwdTile {
   int expert;
   int64_t row0; int rows;     // output rows row0 .. row0 + rows - 1 (one group)
@@ -802,9 +811,9 @@ __device__ __forceinline__ Split fwd_split(const FwdParams& p, int tiles) {
   return split_plan(tiles, p.par, (int)((p.K + STEP - 1) / STEP), p.slots, C::BM * C::BN * 4 / 1024);
 }
 
-// Tile lt whole (PIECES = false), or piece `piece` of S of it into partial
-// slot `slot` (PIECES = true).
-template <class C, bool PIECES>
+// Tile lt whole (PIECES = false; epilogue EPI), or piece `piece` of S of it
+// into partial slot `slot` (PIECES = true).
+template <class C, bool PIECES, int EPI>
 __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int lt, int piece, int S, int slot,
                                         int tiles, const WaveGroups& wg) {
   FwdTile tl;
@@ -838,13 +847,17 @@ __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int l
     store_partial<C>(acc, p.part + (int64_t)slot * (C::BM * C::BN));
   } else {
     ring_mainloop<C>(smem, X, W, wsr, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
-    const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-    uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
-    if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
-      p.out_dtype == MXGG_DTYPE_BF16 ? store_tile_lds<C, true>(acc, smem, o, p.ldo, rows, cols)
-                                     : store_tile_lds<C, false>(acc, smem, o, p.ldo, rows, cols);
-    else
-      store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
+    if constexpr (EPI == kEpiBf16) {
+      store_tile_lds<C, true>(acc, smem, p.out + (row0 * p.ldo + n0) * 2, p.ldo, rows, cols);
+    } else {
+      const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
+      uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
+      if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
+        p.out_dtype == MXGG_DTYPE_BF16 ? store_tile_lds<C, true>(acc, smem, o, p.ldo, rows, cols)
+                                       : store_tile_lds<C, false>(acc, smem, o, p.ldo, rows, cols);
+      else
+        store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
+    }
   }
 }
 
@@ -860,11 +873,12 @@ __device__ __forceinline__ int fwd_groups(const FwdParams& p, WaveGroups& wg) {
   return route_total(p.offs, p.E, C::BM);
 }
 
-// PIECES = false: workgroup i < dp computes tile i whole.  PIECES = true:
-// workgroup u < units computes piece u % S of tile dp + u / S into partial
-// slot u.  Other workgroups exit.  (Two kernels rather than one with both
-// paths: sharing a register allocation slows the whole-tile loop by ~2%.)
-template <class C, bool PIECES>
+// PIECES = false: workgroup i < dp computes tile i whole (epilogue EPI).
+// PIECES = true: workgroup u < units computes piece u % S of tile dp + u / S
+// into partial slot u.  Other workgroups exit.  (Two kernels rather than one
+// with both paths: sharing a register allocation slows the whole-tile loop by
+// ~2%.)
+template <class C, bool PIECES, int EPI = kEpiAny>
 __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   WaveGroups wg;
@@ -872,9 +886,9 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
   const Split sp = fwd_split<C>(p, tiles);
   const int pid = blockIdx.x;
   if constexpr (PIECES) {
-    if (pid < sp.units) fwd_run<C, true>(p, smem, sp.dp + pid / sp.S, pid % sp.S, sp.S, pid, tiles, wg);
+    if (pid < sp.units) fwd_run<C, true, kEpiAny>(p, smem, sp.dp + pid / sp.S, pid % sp.S, sp.S, pid, tiles, wg);
   } else {
-    if (pid < sp.dp) fwd_run<C, false>(p, smem, pid, 0, 1, 0, tiles, wg);
+    if (pid < sp.dp) fwd_run<C, false, EPI>(p, smem, pid, 0, 1, 0, tiles, wg);
   }
 }
 
@@ -980,9 +994,9 @@ __device__ __forceinline__ WgradTile wgrad_tile(const WgradParams& p, int lt) {
 }
 
 // PIECES = false: grid (tiles_n * tiles_k, E), workgroup (x, g) computes tile
-// g * tiles_n * tiles_k + x whole when below dp; true: workgroup u computes
-// piece u % S of tile dp + u / S.
-template <class C, bool PIECES>
+// g * tiles_n * tiles_k + x whole when below dp (epilogue EPI); true:
+// workgroup u computes piece u % S of tile dp + u / S.
+template <class C, bool PIECES, int EPI = kEpiAny>
 __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   int lt, piece = 0;
@@ -1032,12 +1046,16 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
     store_partial<C>(acc, p.part + (int64_t)blockIdx.x * (C::BM * C::BN));
     return;
   }
-  const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-  uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
-  if (esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
-    store_tile_lds<C, true>(acc, smem, o, p.K, rows, cols);   // wgrad: bf16 or f32 only
-  else
-    store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
+  if constexpr (EPI == kEpiBf16) {
+    store_tile_lds<C, true>(acc, smem, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * 2, p.K, rows, cols);
+  } else {
+    const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
+    uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
+    if (esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
+      store_tile_lds<C, true>(acc, smem, o, p.K, rows, cols);   // wgrad: bf16 or f32 only
+    else
+      store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
+  }
 }
 
 // Split tiles of a wgrad launch: one workgroup per item (v, c), as in
@@ -1219,7 +1237,10 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   const int64_t tiles_ub = (int64_t)grid_m_ub * p.grid_n;
   if (tiles_ub <= 0) return MXGG_OK;
   if (tiles_ub > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
-  hipLaunchKernelGGL((fwd_kernel<C, false>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
+  if (p.out_dtype == MXGG_DTYPE_BF16 && p.ldo % 8 == 0 && (uintptr_t)p.out % 16 == 0)
+    hipLaunchKernelGGL((fwd_kernel<C, false, kEpiBf16>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((fwd_kernel<C, false, kEpiAny>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("grouped_mm")) return rc;
   if (!p.slots) return MXGG_OK;
   const int pieces = p.slots < p.par ? p.slots : p.par;   // units <= min(slots, P)
@@ -1478,8 +1499,11 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   p.S = sp.S;
   p.units = sp.units;
   if (sp.dp > 0) {
-    hipLaunchKernelGGL((wgrad_kernel<C, false>), dim3((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E),
-                       dim3(C::NT), 0, st, p);
+    const dim3 grid((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E);
+    if (out_dtype == MXGG_DTYPE_BF16 && K % 8 == 0 && (uintptr_t)out % 16 == 0)
+      hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiBf16>), grid, dim3(C::NT), 0, st, p);
+    else
+      hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiAny>), grid, dim3(C::NT), 0, st, p);
     if (int rc = launch_status("wgrad")) return rc;
   }
   if (!sp.units) return MXGG_OK;
