@@ -220,6 +220,52 @@ def test_fwd_full_size_cfg2(gpu):
     assert sq.item() >= SQNR_GATE
 
 
+def test_fwd_full_size_cfg4_mxfp4(gpu):
+    """BASELINE config 4 at full size: E=8, M=16640, N=8192, K=5120, e4m3
+    activations x packed e2m1 weights (jagged groups), against a GPU fp32
+    dequantize -> per-group matmul of the same quantized operands.  The e2m1
+    codes decode by the OCP MX table (sign bit 3, magnitudes 0 .. 6), element
+    2i in the low nibble."""
+    import random
+
+    import kernels
+    E, M, N, K = 8, 16640, 8192, 5120
+    offs = O.generate_jagged_offs(E, M, 32, rng=random.Random(4))
+    print(f"cfg4 E={E} M={M} N={N} K={K} offs={offs}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(4)
+    a = torch.randn((M, K), device=gpu, generator=g).to(torch.bfloat16)
+    b = (torch.randn((E, N, K), device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    sa, qa = kernels.to_mx(a)
+    sb, qb = kernels.to_mx(b, elem_dtype=torch.float4_e2m1fn_x2)
+    offs_t = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    out = kernels.triton_mxfp8_grouped_mm(qa, qb, sa, sb, offs_t)
+    torch.cuda.synchronize()
+
+    lut = torch.tensor([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6], device=gpu)
+    pb = qb.view(torch.uint8).long()
+    wv = torch.stack([lut[pb & 15], lut[pb >> 4]], dim=-1).reshape(E, N, K)
+    wd = (wv.reshape(E, N, K // 32, 32) * torch.exp2(sb.view(torch.uint8).float() - 127).unsqueeze(-1)).reshape(E, N, K)
+    ad = (qa.float().reshape(M, K // 32, 32) * torch.exp2(sa.view(torch.uint8).float() - 127).unsqueeze(-1)).reshape(M, K)
+    del wv
+    lo = 0
+    err2 = ref2 = 0.0
+    hp_err2 = hp2 = 0.0
+    for e in range(E):
+        hi = offs[e]
+        if hi > lo:
+            ref = ad[lo:hi] @ wd[e].t()
+            o = out[lo:hi].float()
+            err2 += (o - ref).square().sum().item()
+            ref2 += ref.square().sum().item()
+            hp = a[lo:hi].float() @ b[e].float().t()
+            hp_err2 += (o - hp).square().sum().item()
+            hp2 += hp.square().sum().item()
+        lo = hi
+    assert (err2 / ref2) ** 0.5 <= REL_FRO_TIGHT
+    # fp4 weights lose more than fp8 against bf16: a sanity floor only
+    assert 10 * torch.log10(torch.tensor(hp2 / hp_err2)).item() > 12.0
+
+
 # ---------------------------------------------------------------- wgrad
 
 def _wgrad_case(E, M, N, K, offs, gpu, seed=0, out_dtype=torch.bfloat16):
