@@ -50,9 +50,11 @@ constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
 // pieces v*S .. v*S+S-1.
 //
 // Only a last round that follows at most kSplitMaxRounds full rounds is
-// split: after more rounds the whole tiles finish at spread-out times, the
-// last round's tiles start early, and little idle time is left to recover
-// (measured: a loss from 5 full rounds on).  S is picked by a cost model
+// split (measured: a loss from 5 full rounds on).  Tiles of one launch stay
+// in step round after round, so the last round does leave most CUs idle,
+// but its few tiles run uncontended at a higher clock, in about 0.6 of a
+// full round's tile time, and the pieces, the reduce and two more launches
+// cost as much.  S is picked by a cost model
 // (nanoseconds, MI355X kernel traces): the last round of n steps costs about
 // kTailNsPerStep * n (0.75 of 1.7 us per step); cut into S pieces it costs
 // n / S of that, plus kSplitFixedNs (piece prologue and epilogue, two
