@@ -432,9 +432,11 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   read_stage<C>(nxt, snx, (rn / 2) % SCG, Fn, xn, wn);
   // stage r+1 opening scale group g = (r+1)/SPG frees the slot of group g-1
   // (last read, of stage r, before this barrier): group g+1 goes there
-  const bool opens = rn % SPG == 0;
-  issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, wsr, P, s0 / 2 + (rn / SPG + 1) * SCG,
-                  opens);
+  // (a group that starts past the reduction range is never read: not copied,
+  // so the drain after the last stage waits for no memory read)
+  const int tg = s0 / 2 + (rn / SPG + 1) * SCG;
+  const bool opens = rn % SPG == 0 && tg * STEP < hi;
+  issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, wsr, P, tg, opens);
   issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
   mfma_range<C, NE, NMMA>(Fc, xc, wc, acc);
   interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, C::LPS>();
