@@ -976,6 +976,7 @@ struct WgradParams {
   uint8_t* out; int out_dtype;
   int tiles_n; int tiles_k;
   float* part; int dp; int S; int units;    // split plan (host): see split_plan
+  int dev; int par; int slots;              // dev: plan on the device (wgrad_plan) from par, slots
 };
 
 struct WgradTile {
@@ -997,19 +998,56 @@ __device__ __forceinline__ WgradTile wgrad_tile(const WgradParams& p, int lt) {
   return t;
 }
 
+// Reduction steps (of STEP elements) the longest group touches.  Wave-uniform.
+__device__ __forceinline__ int wgrad_max_steps(const int32_t* __restrict__ offs, int E, int64_t M) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int m = 0;
+  for (int base = 0; base < E; base += kWave) {
+    const int e = base + lane;
+    int n = 0;
+    if (e < E) {
+      int lo = e > 0 ? offs[e - 1] : 0;
+      int hi = offs[e];
+      if (lo < 0) lo = 0;
+      if (hi > M) hi = (int)M;
+      n = hi > lo ? (hi + STEP - 1) / STEP - lo / STEP : 0;
+    }
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int o = __shfl_xor(n, d, kWave);
+      n = o > n ? o : n;
+    }
+    m = uniform(n) > m ? uniform(n) : m;
+  }
+  return m;
+}
+
+// Split plan of a wgrad launch: the host's (dev = 0), or, for a lone
+// under-filled round of several groups (dev = 1), one made here from the
+// longest group, which sets the round's length (the host sees only the
+// average).  Every kernel of the launch computes the same plan.
+template <class C>
+__device__ __forceinline__ Split wgrad_plan(const WgradParams& p) {
+  if (!p.dev) return Split{p.dp, p.S, p.units};
+  const int tiles = p.E * p.tiles_n * p.tiles_k;
+  return split_plan(tiles, p.par, wgrad_max_steps(p.offs, p.E, p.M), p.slots, C::BM * C::BN * 4 / 1024);
+}
+
 // PIECES = false: grid (tiles_n * tiles_k, E), workgroup (x, g) computes tile
 // g * tiles_n * tiles_k + x whole when below dp (epilogue EPI); true:
-// workgroup u computes piece u % S of tile dp + u / S.
+// workgroup u < units computes piece u % S of tile dp + u / S (wgrad_plan).
 template <class C, bool PIECES, int EPI = kEpiAny>
 __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
+  const Split sp = wgrad_plan<C>(p);
   int lt, piece = 0;
   if constexpr (PIECES) {
-    lt = p.dp + (int)blockIdx.x / p.S;
-    piece = (int)blockIdx.x % p.S;
+    if ((int)blockIdx.x >= sp.units) return;
+    lt = sp.dp + (int)blockIdx.x / sp.S;
+    piece = (int)blockIdx.x % sp.S;
   } else {
     lt = (int)blockIdx.y * p.tiles_n * p.tiles_k + (int)blockIdx.x;
-    if (lt >= p.dp) return;
+    if (lt >= sp.dp) return;
   }
   const WgradTile tl = wgrad_tile<C>(p, lt);
   const int g = tl.g;
@@ -1023,7 +1061,7 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
     // piece of the group's steps lo/STEP .. cdiv(hi, STEP)-1, clipped to [lo, hi)
     const int a0 = lo / STEP;
     int a, b;
-    split_range(a0, (hi + STEP - 1) / STEP - a0, piece, p.S, a, b);
+    split_range(a0, (hi + STEP - 1) / STEP - a0, piece, sp.S, a, b);
     if (STEP * a > lo) lo = STEP * a;
     if (STEP * b < hi) hi = STEP * b;
   }
@@ -1067,11 +1105,13 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 template <class C>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
   constexpr int CH = ReduceShape<C>::CH;
+  const Split sp = wgrad_plan<C>(p);
   const int v = blockIdx.x / CH, f = (blockIdx.x % CH) * 4 + wave_id();
+  if (sp.S < 2 || v >= sp.units / sp.S) return;
   const int lane = threadIdx.x % kWave;
-  const WgradTile tl = wgrad_tile<C>(p, p.dp + v);
+  const WgradTile tl = wgrad_tile<C>(p, sp.dp + v);
   float acc[16];
-  sum_pieces<C>(p.part + (int64_t)v * p.S * (C::BM * C::BN), p.S, f, lane, acc);
+  sum_pieces<C>(p.part + (int64_t)v * sp.S * (C::BM * C::BN), sp.S, f, lane, acc);
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   store_fragment_lane<C, true>(acc, f, lane, p.out + ((int64_t)tl.g * p.N * p.K + tl.n0 * p.K + tl.k0) * esz,
                                p.K, tl.rows, tl.cols, p.out_dtype);
@@ -1489,7 +1529,7 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   const size_t part_off = align256(need);
   float* part = ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
   WgradParams p{go_t, ld_go, ia_t, ld_ia, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
-                (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0};
+                (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0, 0, 0, 0};
   const int64_t tiles = (int64_t)E * p.tiles_n * p.tiles_k;
   if (tiles > INT32_MAX / 2) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");
   static int resident_cache[64];
@@ -1498,11 +1538,24 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   // only a lone under-filled round is split (its tiles all start at once)
   const bool may_split = E == 1 || tiles < par;
   const int slots = part && may_split ? split_slots<C>(ws_bytes - part_off) : 0;
-  const Split sp = split_plan((int)tiles, par, (int)wgrad_group_steps(E, M), slots, C::BM * C::BN * 4 / 1024);
+  constexpr int kib = C::BM * C::BN * 4 / 1024;
+  const Split sp = split_plan((int)tiles, par, (int)wgrad_group_steps(E, M), slots, kib);
   p.dp = sp.dp;
   p.S = sp.S;
   p.units = sp.units;
-  if (sp.dp > 0) {
+  // A lone round of several groups lasts as long as the longest group, which
+  // only the device knows: the kernels plan from it (wgrad_plan) whenever a
+  // group of all M rows would be split; the grids then cover any plan (every
+  // tile whole, or every tile cut into S <= min(par, slots) / tiles pieces).
+  if (E > 1 && slots > 0 && split_plan((int)tiles, par, (int)cdiv(M, STEP) + 1, slots, kib).units > 0) {
+    p.dev = 1;
+    p.par = par;
+    p.slots = slots;
+  }
+  const int64_t whole_ub = p.dev ? tiles : sp.dp;
+  const int64_t units_ub = p.dev ? (par < slots ? par : slots) : sp.units;
+  const int64_t split_tiles_ub = p.dev ? tiles : (sp.units ? sp.units / sp.S : 0);
+  if (whole_ub > 0) {
     const dim3 grid((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E);
     if (out_dtype == MXGG_DTYPE_BF16 && K % 8 == 0 && (uintptr_t)out % 16 == 0)
       hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiBf16>), grid, dim3(C::NT), 0, st, p);
@@ -1510,10 +1563,10 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
       hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiAny>), grid, dim3(C::NT), 0, st, p);
     if (int rc = launch_status("wgrad")) return rc;
   }
-  if (!sp.units) return MXGG_OK;
-  hipLaunchKernelGGL((wgrad_kernel<C, true>), dim3((unsigned)sp.units), dim3(C::NT), 0, st, p);
+  if (units_ub <= 0) return MXGG_OK;
+  hipLaunchKernelGGL((wgrad_kernel<C, true>), dim3((unsigned)units_ub), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("wgrad")) return rc;
-  hipLaunchKernelGGL((wgrad_reduce_kernel<C>), dim3((unsigned)(sp.units / sp.S * ReduceShape<C>::CH)),
-                     dim3(256), 0, st, p);
+  hipLaunchKernelGGL((wgrad_reduce_kernel<C>), dim3((unsigned)(split_tiles_ub * ReduceShape<C>::CH)), dim3(256),
+                     0, st, p);
   return launch_status("wgrad");
 }
