@@ -108,10 +108,12 @@ __host__ __device__ inline Split split_plan(int T, int P, int nsteps, int slots,
   return sp;
 }
 
-// Steps [a, b) of piece s out of S over steps [a0, a0 + n).
+// Steps [a, b) of piece s out of S over steps [a0, a0 + n).  32-bit
+// unsigned arithmetic: n < 2**25 steps and s < S <= kMaxSplit keep n * (s+1)
+// below 2**28 (a 64-bit division is a long software sequence on the device).
 __host__ __device__ inline void split_range(int a0, int n, int s, int S, int& a, int& b) {
-  a = a0 + (int)((int64_t)n * s / S);
-  b = a0 + (int)((int64_t)n * (s + 1) / S);
+  a = a0 + (int)((uint32_t)n * (uint32_t)s / (uint32_t)S);
+  b = a0 + (int)((uint32_t)n * (uint32_t)(s + 1) / (uint32_t)S);
 }
 
 template <int BM_, int BN_, int WGM_, int WGN_, int WFMT_, int NS_>
@@ -559,9 +561,12 @@ __device__ __forceinline__ void store_tile(const v16f (&acc)[C::FM][C::FN], uint
   }
 }
 
-// fp32 partial tile of a split unit, in accumulator-register order: the 16
-// values of lane l of fragment f = (wave * FM + i) * FN + j at floats
-// (f * 64 + l) * 16 .. +15 of the unit's BM x BN slot (whole-wave 4 KB runs).
+// fp32 partial tile of a split unit, in accumulator-register order: values
+// 4q .. 4q+3 of lane l of fragment f = (wave * FM + i) * FN + j are the float4
+// at index (f * 4 + q) * 64 + l of the unit's BM x BN slot, so every store
+// instruction writes one contiguous 1 KB run.  (With a lane's 16 values
+// contiguous instead, each instruction scatters 64 16-byte pieces over 4 KB
+// and the partial store takes about four times as long.)
 template <class C>
 __device__ __forceinline__ void store_partial(const v16f (&acc)[C::FM][C::FN], float* slot) {
   const int wave = wave_id();
@@ -570,10 +575,11 @@ __device__ __forceinline__ void store_partial(const v16f (&acc)[C::FM][C::FN], f
   for (int i = 0; i < C::FM; ++i)
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
-      float4* d = reinterpret_cast<float4*>(slot + ((int64_t)((wave * C::FM + i) * C::FN + j) * kWave + lane) * 16);
+      float4* d = reinterpret_cast<float4*>(slot) + (int64_t)((wave * C::FM + i) * C::FN + j) * 4 * kWave + lane;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        d[q] = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        d[q * kWave] =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
     }
 }
 
@@ -902,12 +908,12 @@ template <class C>
 __device__ __forceinline__ void sum_pieces(const float* base, int S, int f, int lane, float (&v)[16]) {
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = 0.f;
-  const float* src = base + ((int64_t)f * kWave + lane) * 16;
+  const float4* src = reinterpret_cast<const float4*>(base) + (int64_t)f * 4 * kWave + lane;
   for (int s = 0; s < S; ++s) {
-    const float4* x = reinterpret_cast<const float4*>(src + (int64_t)s * (C::BM * C::BN));
+    const float4* x = src + (int64_t)s * (C::BM * C::BN / 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float4 t = x[q];
+      const float4 t = x[q * kWave];
       v[4 * q] += t.x; v[4 * q + 1] += t.y; v[4 * q + 2] += t.z; v[4 * q + 3] += t.w;
     }
   }
