@@ -68,8 +68,8 @@ constexpr int kMaxSplit = 8;
 constexpr int kMinSplitTotal = 32;
 constexpr int kSplitMaxRounds = 2;
 constexpr int64_t kTailNsPerStep = 1275;
-constexpr int64_t kSplitFixedNs = 12000;
-constexpr int64_t kSplitNsPerMiB = 550;
+constexpr int64_t kSplitFixedNs = 9000;
+constexpr int64_t kSplitNsPerMiB = 400;
 constexpr int64_t kSplitMinGainNs = 16000;
 constexpr size_t kSplitBytes = (size_t)64 << 20;   // partial-tile area of a full workspace
 
