@@ -1039,21 +1039,144 @@ __device__ __forceinline__ Split wgrad_plan(const WgradParams& p) {
   return split_plan(tiles, p.par, wgrad_max_steps(p.offs, p.E, p.M), p.slots, C::BM * C::BN * 4 / 1024);
 }
 
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int o = __shfl_xor(v, d, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Per-group split of a lone wgrad round (dev = 1, E <= 64).  Groups differ in
+// length, and one piece count for every tile leaves the round as long as the
+// longest group's pieces while short groups' tiles idle.  Greedy
+// apportionment instead: from one piece per tile, the first group with the
+// longest pieces gets one more piece per tile, again and again, while the
+// units (E * TNK tiles' pieces, TNK = tiles_n * tiles_k) fit the budget
+// min(par, slots), every piece keeps kMinSplitSteps steps and no tile exceeds
+// kMaxSplit pieces.  Each candidate is priced with split_plan's cost model,
+// the round lasting as long as its longest piece; the best one is kept if it
+// saves kSplitMinGainNs, else no tile is split.  Integer, lane-parallel and
+// deterministic: every workgroup of every kernel of the launch gets the same
+// plan.  Lane g < E holds group g's entries.
+struct WgradGroups {
+  int s;       // pieces per tile of group `lane` (1: whole, as one piece); 0 past E
+  int c0;      // first unit of group `lane`'s tiles (exclusive prefix of TNK * s)
+  int units;   // units in all; 0: no tile is split
+};
+
+template <class C>
+__device__ __forceinline__ WgradGroups wgrad_groups(const WgradParams& p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tnk = p.tiles_n * p.tiles_k;
+  int n = 0;
+  if (lane < p.E) {
+    int lo = lane > 0 ? p.offs[lane - 1] : 0;
+    int hi = p.offs[lane];
+    if (lo < 0) lo = 0;
+    if (hi > p.M) hi = (int)p.M;
+    n = hi > lo ? (hi + STEP - 1) / STEP - lo / STEP : 0;
+    if (n > (1 << 20)) n = 1 << 20;   // keeps the cost model's products in int32
+  }
+  int s = lane < p.E ? 1 : 0, len = n, units = p.E * tnk, best_s = s, best_units = 0;
+  const int budget = p.par < p.slots ? p.par : p.slots;
+  const int len0 = wave_max(len);
+  const int tail = (int)kTailNsPerStep * len0;
+  int best = (int)kSplitMinGainNs;
+  constexpr int kib = C::BM * C::BN * 4 / 1024;
+  if (len0 >= kMinSplitTotal) {
+    for (int it = 0; it < kWave && units + tnk <= budget; ++it) {
+      const int m = wave_max(len);
+      const int g = __builtin_ctzll(__ballot(lane < p.E && len == m));
+      const int gn = lane_value(n, g), gs = lane_value(s, g);
+      if (gs >= kMaxSplit || gn / (gs + 1) < kMinSplitSteps) break;
+      if (lane == g) {
+        s = gs + 1;
+        len = (n + s - 1) / s;
+      }
+      units += tnk;
+      const int gain = tail - (int)kTailNsPerStep * wave_max(len) - (int)kSplitFixedNs -
+                       units * kib * (int)kSplitNsPerMiB / 1024;
+      if (gain > best) {
+        best = gain;
+        best_s = s;
+        best_units = units;
+      }
+    }
+  }
+  WgradGroups w;
+  w.units = best_units;
+  w.s = lane < p.E ? (best_units ? best_s : 1) : 0;
+  w.c0 = wave_incl_scan(tnk * w.s) - tnk * w.s;
+  return w;
+}
+
+// Tiles below the returned index run whole (PIECES = false).
+template <class C>
+__device__ __forceinline__ int wgrad_whole(const WgradParams& p) {
+  if (p.dev && p.E <= kWave) return wgrad_groups<C>(p).units ? 0 : p.E * p.tiles_n * p.tiles_k;
+  return wgrad_plan<C>(p).dp;
+}
+
+// Tile, piece and piece count of unit u of the piece kernel; false past the
+// plan's units.  Unit u writes partial slot u; a tile's pieces are
+// consecutive units.
+template <class C>
+__device__ __forceinline__ bool wgrad_unit(const WgradParams& p, int u, int& lt, int& piece, int& S) {
+  if (p.dev && p.E <= kWave) {
+    const WgradGroups w = wgrad_groups<C>(p);
+    if (u >= w.units) return false;
+    const int tnk = p.tiles_n * p.tiles_k;
+    const int g = __builtin_ctzll(__ballot(w.s > 0 && w.c0 + tnk * w.s > u));
+    S = lane_value(w.s, g);
+    const int r = u - lane_value(w.c0, g);
+    lt = g * tnk + r / S;
+    piece = r % S;
+    return true;
+  }
+  const Split sp = wgrad_plan<C>(p);
+  if (u >= sp.units) return false;
+  lt = sp.dp + u / sp.S;
+  piece = u % sp.S;
+  S = sp.S;
+  return true;
+}
+
+// Split tile v of the reduce kernel: its tile, first partial slot and piece
+// count; false past the split tiles.
+template <class C>
+__device__ __forceinline__ bool wgrad_split_tile(const WgradParams& p, int v, int& lt, int& base, int& S) {
+  if (p.dev && p.E <= kWave) {
+    const WgradGroups w = wgrad_groups<C>(p);
+    const int tnk = p.tiles_n * p.tiles_k;
+    if (!w.units || v >= p.E * tnk) return false;
+    const int g = v / tnk;
+    S = lane_value(w.s, g);
+    base = lane_value(w.c0, g) + (v - g * tnk) * S;
+    lt = v;
+    return true;
+  }
+  const Split sp = wgrad_plan<C>(p);
+  if (sp.S < 2 || v >= sp.units / sp.S) return false;
+  lt = sp.dp + v;
+  base = v * sp.S;
+  S = sp.S;
+  return true;
+}
+
 // PIECES = false: grid (tiles_n * tiles_k, E), workgroup (x, g) computes tile
-// g * tiles_n * tiles_k + x whole when below dp (epilogue EPI); true:
-// workgroup u < units computes piece u % S of tile dp + u / S (wgrad_plan).
+// g * tiles_n * tiles_k + x whole when below wgrad_whole (epilogue EPI);
+// true: workgroup u computes the piece wgrad_unit assigns it.
 template <class C, bool PIECES, int EPI = kEpiAny>
 __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
-  const Split sp = wgrad_plan<C>(p);
-  int lt, piece = 0;
+  int lt, piece = 0, S = 1;
   if constexpr (PIECES) {
-    if ((int)blockIdx.x >= sp.units) return;
-    lt = sp.dp + (int)blockIdx.x / sp.S;
-    piece = (int)blockIdx.x % sp.S;
+    if (!wgrad_unit<C>(p, (int)blockIdx.x, lt, piece, S)) return;
   } else {
     lt = (int)blockIdx.y * p.tiles_n * p.tiles_k + (int)blockIdx.x;
-    if (lt >= sp.dp) return;
+    if (lt >= wgrad_whole<C>(p)) return;
   }
   const WgradTile tl = wgrad_tile<C>(p, lt);
   const int g = tl.g;
@@ -1067,7 +1190,7 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
     // piece of the group's steps lo/STEP .. cdiv(hi, STEP)-1, clipped to [lo, hi)
     const int a0 = lo / STEP;
     int a, b;
-    split_range(a0, (hi + STEP - 1) / STEP - a0, piece, sp.S, a, b);
+    split_range(a0, (hi + STEP - 1) / STEP - a0, piece, S, a, b);
     if (STEP * a > lo) lo = STEP * a;
     if (STEP * b < hi) hi = STEP * b;
   }
@@ -1107,17 +1230,17 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 }
 
 // Split tiles of a wgrad launch: one workgroup per item (v, c), as in
-// fwd_reduce_kernel; the grid is exact (the plan is the host's).
+// fwd_reduce_kernel; items past the plan's split tiles exit.
 template <class C>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
   constexpr int CH = ReduceShape<C>::CH;
-  const Split sp = wgrad_plan<C>(p);
   const int v = blockIdx.x / CH, f = (blockIdx.x % CH) * 4 + wave_id();
-  if (sp.S < 2 || v >= sp.units / sp.S) return;
+  int lt, base, S;
+  if (!wgrad_split_tile<C>(p, v, lt, base, S)) return;
   const int lane = threadIdx.x % kWave;
-  const WgradTile tl = wgrad_tile<C>(p, sp.dp + v);
+  const WgradTile tl = wgrad_tile<C>(p, lt);
   float acc[16];
-  sum_pieces<C>(p.part + (int64_t)v * sp.S * (C::BM * C::BN), sp.S, f, lane, acc);
+  sum_pieces<C>(p.part + (int64_t)base * (C::BM * C::BN), S, f, lane, acc);
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   store_fragment_lane<C, true>(acc, f, lane, p.out + ((int64_t)tl.g * p.N * p.K + tl.n0 * p.K + tl.k0) * esz,
                                p.K, tl.rows, tl.cols, p.out_dtype);

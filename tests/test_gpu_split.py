@@ -151,6 +151,7 @@ def _wgrad_abi(qg, sg, qi, si, offs_t, out_dtype, ws_bytes):
     (1, 8192, 512, 512, [8192], torch.bfloat16),               # 4 tiles, 64 steps -> 8 pieces
     (3, 24576, 320, 288, [0, 8000, 24576], torch.bfloat16),    # empty group, bounds not at 128
     (2, 16384, 256, 512, [8160, 16384], torch.float32),        # f32 out (bf16-rounded values)
+    (2, 16384, 512, 512, [1024, 16384], torch.bfloat16),       # 8 vs 120 steps: per-group piece counts
 ])
 def test_wgrad_split_matches_whole_tiles(gpu, E, M, N, K, offs, out_dtype):
     import kernels
