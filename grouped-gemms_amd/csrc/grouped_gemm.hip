@@ -30,6 +30,8 @@
 //     stages; each MFMA takes its lane's byte at op_sel 0.
 //   * one workgroup barrier per stage; fragment and scale registers alternate
 //     between two sets (loop body unrolled twice).
+#include <type_traits>
+
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
@@ -776,6 +778,7 @@ struct FwdParams {
   uint8_t* out; int out_dtype; int64_t ldo;
   int grid_n; int group_m; int xcd;
   float* part; int par; int slots;          // split: partial slots, resident workgroups, slot count
+  int quads;                                // last round as 128 x 128 quarter tiles (quad_dp)
 };
 
 // Epilogue of the whole-tile kernels, fixed at compile time so that the
@@ -816,18 +819,30 @@ __device__ __forceinline__ bool fwd_tile(const FwdParams& p, int lt, int tiles, 
   return true;
 }
 
+// Tiles of a 256 x 256 launch computed whole when its last round runs as
+// 128 x 128 quarter tiles (fwd_quad_kernel): a reduction too short to split
+// (fewer than kMinSplitTotal steps), at most kSplitMaxRounds full rounds
+// before it, and four quarters per tile of the rem = T % P tiles fit one
+// round.  A lone round of 256 x 256 tiles at K = 2048 takes about as long as
+// a full round (42 us against 38; the copies of one tile per CU are latency
+// bound), its quarters on four times the CUs about 60% of that.
+__host__ __device__ inline int quad_dp(int T, int P) {
+  if (T <= 0 || P <= 0 || T / P > kSplitMaxRounds) return T;
+  const int rem = T % P;
+  return rem > 0 && 4 * rem <= P ? T - rem : T;
+}
+
 template <class C>
 __device__ __forceinline__ Split fwd_split(const FwdParams& p, int tiles) {
+  if (p.quads) return Split{quad_dp(tiles, p.par), 1, 0};
   return split_plan(tiles, p.par, (int)((p.K + STEP - 1) / STEP), p.slots, C::BM * C::BN * 4 / 1024);
 }
 
-// Tile lt whole (PIECES = false; epilogue EPI), or piece `piece` of S of it
+// Tile tl whole (PIECES = false; epilogue EPI), or piece `piece` of S of it
 // into partial slot `slot` (PIECES = true).
 template <class C, bool PIECES, int EPI>
-__device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int lt, int piece, int S, int slot,
-                                        int tiles, const WaveGroups& wg) {
-  FwdTile tl;
-  if (!fwd_tile<C>(p, lt, tiles, wg, tl)) return;
+__device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, const FwdTile& tl, int piece, int S,
+                                             int slot) {
   const int64_t row0 = tl.row0, n0 = tl.n0;
   const int rows = tl.rows, cols = tl.cols;
 
@@ -871,6 +886,14 @@ __device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int l
   }
 }
 
+// Tile of logical index lt, run as fwd_tile_run describes.
+template <class C, bool PIECES, int EPI>
+__device__ __forceinline__ void fwd_run(const FwdParams& p, uint8_t* smem, int lt, int piece, int S, int slot,
+                                        int tiles, const WaveGroups& wg) {
+  FwdTile tl;
+  if (fwd_tile<C>(p, lt, tiles, wg, tl)) fwd_tile_run<C, PIECES, EPI>(p, smem, tl, piece, S, slot);
+}
+
 // Groups of a forward launch and its m-block count: one read of offs when
 // E <= 64 (kept for the tile lookup), else a scan of offs in 64-group chunks.
 template <class C>
@@ -900,6 +923,30 @@ __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
   } else {
     if (pid < sp.dp) fwd_run<C, false, EPI>(p, smem, pid, 0, 1, 0, tiles, wg);
   }
+}
+
+// The last round of a launch of C tiles (256 x 256) as Q tiles (128 x 128):
+// workgroup u < 4 * (tiles - dp) computes quarter u % 4 (row half u / 2 % 2,
+// column half u % 2) of tile dp + u / 4, clipped to the tile; the routing and
+// the plan are C's, so the whole-tile kernel and this one agree on dp.
+template <class C, class Q, int EPI>
+__global__ __launch_bounds__(Q::NT) void fwd_quad_kernel(FwdParams p) {
+  static_assert(C::BM == 2 * Q::BM && C::BN == 2 * Q::BN && C::WFMT == Q::WFMT, "quarter tiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Q::LDS];
+  WaveGroups wg;
+  const int tiles = fwd_groups<C>(p, wg) * p.grid_n;
+  const int dp = fwd_split<C>(p, tiles).dp;
+  const int u = blockIdx.x;
+  if (u >= 4 * (tiles - dp)) return;
+  FwdTile tl;
+  if (!fwd_tile<C>(p, dp + u / 4, tiles, wg, tl)) return;
+  const int dr = (u & 2) ? Q::BM : 0, dc = (u & 1) ? Q::BN : 0;
+  if (tl.rows <= dr || tl.cols <= dc) return;
+  tl.row0 += dr;
+  tl.rows = tl.rows - dr < Q::BM ? tl.rows - dr : Q::BM;
+  tl.n0 += dc;
+  tl.cols = tl.cols - dc < Q::BN ? tl.cols - dc : Q::BN;
+  fwd_tile_run<Q, false, EPI>(p, smem, tl, 0, 1, 0);
 }
 
 // Sum over the S pieces (slots base + s * BM * BN, s = 0 .. S-1, in that
@@ -1407,14 +1454,36 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
     if (est > INT32_MAX || split_plan((int)est, p.par, nsteps, p.slots, C::BM * C::BN * 4 / 1024).units == 0)
       p.slots = 0;
   }
+  // A reduction too short to split: the last round may run as 128 x 128
+  // quarter tiles (quad_dp).  The device decides from the real tile count;
+  // the host, from the usual one, only skips the launch where it cannot help.
+  p.quads = 0;
+  if constexpr (std::is_same<C, CfgF8_256>::value) {
+    if (nsteps < kMinSplitTotal && p.par > 0) {
+      const int64_t est = (cdiv(p.M, C::BM) + (p.E - 1) / 2) * p.grid_n;
+      if (est <= INT32_MAX && quad_dp((int)est, p.par) < est) p.quads = 1;
+    }
+  }
   const int64_t tiles_ub = (int64_t)grid_m_ub * p.grid_n;
   if (tiles_ub <= 0) return MXGG_OK;
   if (tiles_ub > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
-  if (p.out_dtype == MXGG_DTYPE_BF16 && p.ldo % 8 == 0 && (uintptr_t)p.out % 16 == 0)
+  const bool bf16 = p.out_dtype == MXGG_DTYPE_BF16 && p.ldo % 8 == 0 && (uintptr_t)p.out % 16 == 0;
+  if (bf16)
     hipLaunchKernelGGL((fwd_kernel<C, false, kEpiBf16>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
   else
     hipLaunchKernelGGL((fwd_kernel<C, false, kEpiAny>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("grouped_mm")) return rc;
+  if constexpr (std::is_same<C, CfgF8_256>::value) {
+    if (p.quads) {   // 4 * (T % P) <= P quarters
+      if (bf16)
+        hipLaunchKernelGGL((fwd_quad_kernel<C, CfgF8_128, kEpiBf16>), dim3((unsigned)p.par), dim3(CfgF8_128::NT),
+                           0, st, p);
+      else
+        hipLaunchKernelGGL((fwd_quad_kernel<C, CfgF8_128, kEpiAny>), dim3((unsigned)p.par), dim3(CfgF8_128::NT),
+                           0, st, p);
+      if (int rc = launch_status("grouped_mm")) return rc;
+    }
+  }
   if (!p.slots) return MXGG_OK;
   const int pieces = p.slots < p.par ? p.slots : p.par;   // units <= min(slots, P)
   hipLaunchKernelGGL((fwd_kernel<C, true>), dim3((unsigned)pieces), dim3(C::NT), 0, st, p);

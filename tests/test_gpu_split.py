@@ -127,6 +127,72 @@ def test_fwd_split_tail_full_size(gpu):
     assert (d <= 2.0 ** -6 * whole.float().abs().amax(dim=1).clamp_min(1.0)).all()
 
 
+# ------------------------------------------------- quarter-tile last round
+#
+# A reduction under 32 steps is never split; instead, a last round of at most
+# P / 4 tiles of 256 x 256 after at most two full rounds runs as 128 x 128
+# quarter tiles (quad_dp).  The small cases below have far fewer than P / 4
+# tiles (P = resident workgroups, 256 on MI355X), so every tile is quartered;
+# quarters compute each output element with the same MFMA sequence as a
+# 128 x 128 launch, so the two agree bit for bit.
+
+@pytest.mark.parametrize("E,M,N,K,out_dtype", [
+    (3, 992, 300, 1024, torch.bfloat16),      # empty group, partial quarters in rows and columns
+    (4, 2048, 512, 2048, torch.float32),      # f32 out
+    (2, 608, 256, 128, torch.float16),        # one step, f16 out
+])
+def test_fwd_quarter_tiles(gpu, E, M, N, K, out_dtype):
+    import kernels
+    from kernels import _lib
+    offs = seeded_offs(E, M, seed=E * 17 + K)
+    if E >= 3:
+        offs[1] = offs[0]
+    offs_t = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    sa, qa = kernels.to_mx(randn_bf16((M, K), 1.0, 3 + K).to(gpu))
+    sb, qb = kernels.to_mx(randn_bf16((E, N, K), 0.05, 4 + K).to(gpu))
+    full = _lib.load().mxgg_grouped_mm_workspace_size(E, M, N, K)
+    quarters = _fwd_abi(qa, sa, qb, sb, offs_t, _lib.FMT_E4M3, out_dtype, full, 256)
+    small = _fwd_abi(qa, sa, qb, sb, offs_t, _lib.FMT_E4M3, out_dtype, full, 128)
+    rows = offs[-1]
+    assert torch.equal(quarters[:rows], small[:rows])
+    ref = O.grouped_mm(bits_u8(qa), bits_u8(sa), bits_u8(qb), bits_u8(sb), offs)
+    o = f32(quarters)[:rows]
+    assert np.isfinite(o).all()
+    assert O.rel_fro(ref[:rows], o) <= REL_FRO_TIGHT
+
+
+@pytest.mark.parametrize("E", [1, 8])
+def test_fwd_quarter_tail_full_size(gpu, E):
+    """M=16640, N=K=2048 with 256 x 256 tiles: 520 (E=1) or about 550 (E=8,
+    jagged) tiles -- two full rounds on 256 CUs and a last round of quarter
+    tiles.  Against a GPU fp32 dequantize -> matmul per group."""
+    import kernels
+    from kernels import _lib
+    M, N, K = 16640, 2048, 2048
+    g = torch.Generator(device=gpu).manual_seed(11 + E)
+    a = torch.randn((M, K), device=gpu, generator=g).to(torch.bfloat16)
+    b = (torch.randn((E, N, K), device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    sa, qa = kernels.to_mx(a)
+    sb, qb = kernels.to_mx(b)
+    offs = seeded_offs(E, M, seed=E) if E > 1 else [M]
+    offs_t = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    full = _lib.load().mxgg_grouped_mm_workspace_size(E, M, N, K)
+    out = _fwd_abi(qa, sa, qb, sb, offs_t, _lib.FMT_E4M3, torch.bfloat16, full, 256)
+
+    def deq(q, s):
+        v = q.float().reshape(*q.shape[:-1], -1, 32)
+        return (v * torch.exp2(s.float() - 127).unsqueeze(-1)).reshape(q.shape)
+
+    da, db = deq(qa, sa), deq(qb, sb)
+    lo = 0
+    for e, hi in enumerate(offs):
+        if hi > lo:
+            ref = da[lo:hi] @ db[e].t()
+            err = (out[lo:hi].float() - ref).norm() / ref.norm()
+            assert err.item() <= REL_FRO_TIGHT, (e, lo, hi, err.item())
+        lo = hi
+
+
 # ---------------------------------------------------------------- wgrad
 
 def _wgrad_abi(qg, sg, qi, si, offs_t, out_dtype, ws_bytes):
