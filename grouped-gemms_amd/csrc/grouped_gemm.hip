@@ -5,6 +5,8 @@
 //   * scale re-layout feeding both GEMMs                    (the role of kernels/forward.py:367-397)
 //   * split of an under-filled last round along the reduction, with fp32
 //     partial tiles and a reduce kernel        (generalises kernels/backward.py:106-215)
+//   * forward last round with a reduction too short to split as 128 x 128
+//     quarter tiles (fwd_quad_kernel)
 //
 // Both GEMMs are "NT" products whose two operands are contiguous along the
 // reduction dimension, so they share one main loop:
@@ -1029,7 +1031,7 @@ struct WgradParams {
   uint8_t* out; int out_dtype;
   int tiles_n; int tiles_k;
   float* part; int dp; int S; int units;    // split plan (host): see split_plan
-  int dev; int par; int slots;              // dev: plan on the device (wgrad_plan) from par, slots
+  int dev; int par; int slots;              // dev: plan on the device (wgrad_groups / wgrad_plan) from par, slots
 };
 
 struct WgradTile {
@@ -1742,9 +1744,10 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   p.S = sp.S;
   p.units = sp.units;
   // A lone round of several groups lasts as long as the longest group, which
-  // only the device knows: the kernels plan from it (wgrad_plan) whenever a
-  // group of all M rows would be split; the grids then cover any plan (every
-  // tile whole, or every tile cut into S <= min(par, slots) / tiles pieces).
+  // only the device knows: the kernels plan from the groups' lengths
+  // (wgrad_groups, or wgrad_plan past 64 groups) whenever a group of all M
+  // rows would be split.  The grids cover any such plan: every tile whole, or
+  // at most min(par, slots) pieces and every tile reduced.
   if (E > 1 && slots > 0 && split_plan((int)tiles, par, (int)cdiv(M, STEP) + 1, slots, kib).units > 0) {
     p.dev = 1;
     p.par = par;
