@@ -48,10 +48,13 @@ constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
 // at once, the rem = T % P tiles of the last round leave most of the chip idle
 // for (a fraction of) a tile time.  They can instead be cut into S pieces
 // along the reduction (whole 128-element steps, at least kMinSplitSteps per
-// piece, at most kMaxSplit pieces per tile, S <= P / rem, `slots` pieces in
-// all); pieces store fp32 partial tiles and a second kernel adds them in
-// piece order and rounds once.  Tiles 0 .. dp-1 run whole, tile dp + v as
-// pieces v*S .. v*S+S-1.
+// piece, at most kMaxSplit pieces per tile, `slots` pieces in all); pieces
+// store fp32 partial tiles and a second kernel adds them in piece order and
+// rounds once.  Tiles 0 .. dp-1 run whole, tile dp + v as pieces v*S ..
+// v*S+S-1.  Up to P / 2 last-round tiles, S <= P / rem keeps the pieces in one
+// round.  Past that, S pieces per tile run in ceil(rem * S / P) rounds (160
+// tiles on 256 CUs: 3 pieces each, two rounds of a third of the reduction
+// instead of one round of all of it).
 //
 // Only a last round that follows at most kSplitMaxRounds full rounds is
 // split (measured: a loss from 5 full rounds on).  Tiles of one launch stay
@@ -60,8 +63,9 @@ constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
 // full round's tile time, and the pieces, the reduce and two more launches
 // cost as much.  S is picked by a cost model
 // (nanoseconds, MI355X kernel traces): the last round of n steps costs about
-// kTailNsPerStep * n (0.75 of 1.7 us per step); cut into S pieces it costs
-// n / S of that, plus kSplitFixedNs (piece prologue and epilogue, two
+// kTailNsPerStep * n (0.75 of 1.7 us per step; kBusyNsPerStep, 1.7 us, when
+// the last round fills more than half the chip); cut into S pieces it costs
+// rounds * n / S of that, plus kSplitFixedNs (piece prologue and epilogue, two
 // launches) plus the partial traffic, rem * S tiles written and read back
 // (kSplitNsPerMiB).  No split unless that saves at least kSplitMinGainNs (the
 // model is coarse); reductions shorter than kMinSplitTotal steps are never
@@ -72,10 +76,11 @@ constexpr int kMaxSplit = 8;
 constexpr int kMinSplitTotal = 32;
 constexpr int kSplitMaxRounds = 2;
 constexpr int64_t kTailNsPerStep = 1275;
+constexpr int64_t kBusyNsPerStep = 1700;
 constexpr int64_t kSplitFixedNs = 9000;
 constexpr int64_t kSplitNsPerMiB = 400;
 constexpr int64_t kSplitMinGainNs = 16000;
-constexpr size_t kSplitBytes = (size_t)64 << 20;   // partial-tile area of a full workspace
+constexpr size_t kSplitBytes = (size_t)128 << 20;  // partial-tile area of a full workspace
 
 struct Split {
   int dp;       // tiles computed whole
@@ -88,19 +93,23 @@ __host__ __device__ inline Split split_plan(int T, int P, int nsteps, int slots,
   if (T <= 0 || P <= 0 || nsteps < kMinSplitTotal || T / P > kSplitMaxRounds) return sp;
   const int rem = T % P;
   if (rem == 0) return sp;
-  int smax = P / rem;
+  int smax = 2 * rem > P ? kMaxSplit : P / rem;
   if (smax > kMaxSplit) smax = kMaxSplit;
   if (smax > nsteps / kMinSplitSteps) smax = nsteps / kMinSplitSteps;
   if (smax > slots / rem) smax = slots / rem;
-  // int32 throughout: tail < 1275 * 2^20, and rem * S <= slots <= 4096 with
-  // tile_kib <= 256 keeps the staging term below 2^30.  Unrolled, every
+  // int32 throughout: tail <= 1700 * 2^20, rounds * (tail / S) <= tail, and
+  // rem * S <= slots <= 4096 with tile_kib <= 256 keeps the staging term
+  // below 2^30.  Unrolled, every
   // tail / S has a constant divisor.
-  const int tail = (int)kTailNsPerStep * (nsteps < (1 << 20) ? nsteps : (1 << 20));
+  const int per = (int)(2 * rem > P ? kBusyNsPerStep : kTailNsPerStep);
+  const int tail = per * (nsteps < (1 << 20) ? nsteps : (1 << 20));
   int best = (int)kSplitMinGainNs;
 #pragma unroll
   for (int S = 2; S <= kMaxSplit; ++S) {
     if (S > smax) break;
-    const int gain = tail - tail / S - (int)kSplitFixedNs - rem * S * tile_kib * (int)kSplitNsPerMiB / 1024;
+    const int rounds = (rem * S + P - 1) / P;   // <= S while rem < P
+    const int gain =
+        tail - rounds * (tail / S) - (int)kSplitFixedNs - rem * S * tile_kib * (int)kSplitNsPerMiB / 1024;
     if (gain > best) {
       best = gain;
       sp.S = S;
@@ -1487,7 +1496,7 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
     }
   }
   if (!p.slots) return MXGG_OK;
-  const int pieces = p.slots < p.par ? p.slots : p.par;   // units <= min(slots, P)
+  const int pieces = p.slots;   // units = rem * S <= slots
   hipLaunchKernelGGL((fwd_kernel<C, true>), dim3((unsigned)pieces), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("grouped_mm")) return rc;
   // a split needs rem <= par / 2 tiles of ReduceShape::CH items each; a small
@@ -1754,7 +1763,7 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
     p.slots = slots;
   }
   const int64_t whole_ub = p.dev ? tiles : sp.dp;
-  const int64_t units_ub = p.dev ? (par < slots ? par : slots) : sp.units;
+  const int64_t units_ub = p.dev ? slots : sp.units;
   const int64_t split_tiles_ub = p.dev ? tiles : (sp.units ? sp.units / sp.S : 0);
   if (whole_ub > 0) {
     const dim3 grid((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E);

@@ -161,7 +161,7 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            them per call too, kernels/forward.py:537-550).  Recommended:
  *            mxgg_grouped_mm_workspace_size(E, M, N, K) bytes, which adds (after
  *            the scales, 256-byte aligned) room for the fp32 partial tiles of a
- *            last, partial round of tiles cut along K (at most 64 MiB; only for
+ *            last, partial round of tiles cut along K (at most 128 MiB; only for
  *            K >= 4096 and short launches).  With less, no tile is cut.
  * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
  * rows need no alignment.  Results do not depend on the workspace size beyond

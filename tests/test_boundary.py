@@ -97,15 +97,15 @@ def test_grouped_mm_validation_without_gpu(args, needle):
 def test_grouped_mm_workspace_without_gpu():
     """Workspace = the re-laid scales (4 * ceil(red/128) bytes per operand
     row), then, 256-byte aligned, the fp32 partial tiles of a split last round
-    when the reduction has >= 32 steps of 128: at most 64 MiB, and no more than
+    when the reduction has >= 32 steps of 128: at most 128 MiB, and no more than
     every tile cut into min(8, steps // 4) pieces (256x256 or 128x128 tiles,
     whichever needs more).  A call without the scale part is rejected
     (MXGG_ERR_WORKSPACE) before any HIP call."""
     from kernels import _lib
     lib = _lib.load()
     MiB = 1 << 20
-    # E=8, M=16640, N=8192, K=5120: 40 steps; thousands of tiles -> the 64 MiB cap
-    assert lib.mxgg_grouped_mm_workspace_size(8, 16640, 8192, 5120) == 4 * 40 * (16640 + 8 * 8192) + 64 * MiB
+    # E=8, M=16640, N=8192, K=5120: 40 steps; thousands of tiles -> the 128 MiB cap
+    assert lib.mxgg_grouped_mm_workspace_size(8, 16640, 8192, 5120) == 4 * 40 * (16640 + 8 * 8192) + 128 * MiB
     # K=160: 2 steps, K=2048: 16 steps -- too short to split -> scales only, unaligned
     assert lib.mxgg_grouped_mm_workspace_size(1, 100, 64, 160) == 4 * 2 * (100 + 64)
     assert lib.mxgg_grouped_mm_workspace_size(2, 1000, 300, 2048) == 4 * 16 * (1000 + 2 * 300)
@@ -113,7 +113,7 @@ def test_grouped_mm_workspace_without_gpu():
     # four 128x128 tiles (32 x 64 KiB): 2 MiB after 65536 bytes of scales
     assert lib.mxgg_grouped_mm_workspace_size(1, 256, 256, 4096) == 4 * 32 * (256 + 256) + 2 * MiB
     # wgrad E=4, M=16640: 33 steps per average group -> 8 pieces; 640 tiles -> cap
-    assert lib.mxgg_wgrad_workspace_size(4, 16640, 2048, 5120) == 4 * 130 * (2048 + 5120) + 64 * MiB
+    assert lib.mxgg_wgrad_workspace_size(4, 16640, 2048, 5120) == 4 * 130 * (2048 + 5120) + 128 * MiB
     # wgrad E=8, M=16640: 17 steps per average group -> no split
     assert lib.mxgg_wgrad_workspace_size(8, 16640, 256, 256) == 4 * 130 * (256 + 256)
     rc = lib.mxgg_grouped_mm(16, 64, 16, 2, 16, 0, 64, 64 * 64, 16, 2, 128, 16, 1, 64, 64, 64,

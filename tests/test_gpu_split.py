@@ -218,6 +218,7 @@ def _wgrad_abi(qg, sg, qi, si, offs_t, out_dtype, ws_bytes):
     (3, 24576, 320, 288, [0, 8000, 24576], torch.bfloat16),    # empty group, bounds not at 128
     (2, 16384, 256, 512, [8160, 16384], torch.float32),        # f32 out (bf16-rounded values)
     (2, 16384, 512, 512, [1024, 16384], torch.bfloat16),       # 8 vs 120 steps: per-group piece counts
+    (1, 16640, 2560, 3584, [16640], torch.bfloat16),           # 140 tiles > P / 2: pieces in two rounds
 ])
 def test_wgrad_split_matches_whole_tiles(gpu, E, M, N, K, offs, out_dtype):
     import kernels
