@@ -946,7 +946,9 @@ __global__ __launch_bounds__(Q::NT) void fwd_quad_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Q::LDS];
   WaveGroups wg;
   const int tiles = fwd_groups<C>(p, wg) * p.grid_n;
-  const int dp = fwd_split<C>(p, tiles).dp;
+  const Split sp = fwd_split<C>(p, tiles);
+  if (sp.units) return;   // a last round split into pieces is not quartered
+  const int dp = sp.dp;
   const int u = blockIdx.x;
   if (u >= 4 * (tiles - dp)) return;
   FwdTile tl;
