@@ -149,18 +149,20 @@ struct Cfg {
   static constexpr int XBYTES = BM * XROW;
   static constexpr int WBYTES = BN * WROW;
   static constexpr int STAGE = XBYTES + WBYTES;
-  // scale ring after the data ring: two slots of SCG steps x (BM X rows, then
-  // BN W rows) dwords
+  // scale ring after the data ring: two slots, each SCG steps x BM X-row
+  // dwords ([step][row]) followed by SCG steps x BN W-row dwords
   static constexpr int SSLOT = SCG * (BM + BN) * 4;
   static constexpr int SOFF = NS * STAGE;
   static constexpr int LDS = SOFF + 2 * SSLOT;
   static constexpr int QX = XBYTES / 1024 / NW;     // 1 KB data copies per wave and stage
   static constexpr int QW = WBYTES / 1024 / NW;
   static constexpr int LPS = QX + QW;               // LDS-DMA loads per wave and stage
-  static constexpr int NSD = SSLOT / 1024;          // 1 KB scale copies per group
+  static constexpr int NSX = SCG * BM * 4 / 1024;   // 1 KB scale copies of the X part (waves 0 ..)
+  static constexpr int NSD = SSLOT / 1024;          // 1 KB scale copies per group (X, then W)
   static_assert(XBYTES % (1024 * NW) == 0 && WBYTES % (1024 * NW) == 0, "tile/wave split");
-  static_assert(SSLOT % 1024 == 0 && NSD <= NW, "scale copies: at most one per wave");
-  static_assert(BM % 4 == 0 && (BM + BN) % 4 == 0, "scale pieces stay in one operand and step");
+  static_assert((SCG * BM * 4) % 1024 == 0 && (SCG * BN * 4) % 1024 == 0 && NSD <= NW,
+                "scale copies: one operand each, at most one per wave");
+  static_assert(BM % 4 == 0 && BN % 4 == 0, "scale pieces stay in one step");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(NS >= 3 && LDS <= 160 * 1024, "ring depth / LDS budget");
   // a scale group is copied SPG - 1 stages before its first read; the wait
@@ -183,10 +185,12 @@ struct Operand {
   uint32_t ld;                   // bytes between rows
 };
 
-// Where a tile's re-laid scales live: dword (t, r) of an operand with R rows
-// per step is at byte off + 4 (t R + r) of the workspace.
+// Where a tile's step-major scales live: dword (t, r) of an operand with R
+// rows per step is at byte 4 (t R + r) of the buffer `rsrc` (the operand's
+// [step][row] array, re-laid into the workspace or written so by the
+// quantizer); reads past the buffer return 0.
 struct ScaleSrc {
-  uint32_t off;     // byte offset of the operand's [step][row] array in the workspace
+  __amdgpu_buffer_rsrc_t rsrc;
   uint32_t rows;    // R: rows per step of that array
   uint32_t row0;    // first row of the tile
 };
@@ -205,8 +209,9 @@ struct Frags {
 // lane's offset is at most 31 rows of a stride below 2**23 plus 48 bytes:
 // below 2**28).
 // Scale copy of wave w (w < NSD): slot dwords 256 w .. 256 w + 255, 4 per
-// lane; lane l covers step u and tile row v of the group, at workspace byte
-// s_base + t * s_step for step t of the reduction.
+// lane, of the X part (w < NSX) or the W part; lane l covers step u and tile
+// rows r .. r+3 of its operand, at byte s_base + t * s_step of that
+// operand's scale buffer for step t of the reduction.
 template <class C>
 struct Plan {
   uint32_t xoff;
@@ -233,14 +238,15 @@ __device__ __forceinline__ void make_plan(Plan<C>& P, const Operand& X, const Op
     const int c = (lane & 3) ^ swz4(row);
     P.woff = ((uint32_t)row * W.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
   }
-  const int q = wave_id() * 256 + 4 * lane;       // first slot dword of the lane
-  const int u = q / (C::BM + C::BN);              // step of the group
-  const int v = q % (C::BM + C::BN);              // tile row: X rows, then W rows
-  const bool isx = v < C::BM;
+  const int wave = wave_id();
+  const bool isx = wave < C::NSX;
+  const int R = isx ? C::BM : C::BN;              // tile rows of the lane's operand
+  const int q = (isx ? wave : wave - C::NSX) * 256 + 4 * lane;   // first dword of the lane in its part
+  const int u = q / R;                            // step of the group
   const ScaleSrc& S = isx ? xs : ws;
-  const uint32_t r = S.row0 + (uint32_t)(isx ? v : v - C::BM);
+  const uint32_t r = S.row0 + (uint32_t)(q % R);
   P.s_step = S.rows * 4u;
-  P.s_base = S.off + r * 4u + (uint32_t)u * P.s_step;
+  P.s_base = r * 4u + (uint32_t)u * P.s_step;
 }
 
 // Global -> LDS copies of stage `st` (elements [64 st, 64 st + 64)) into slot
@@ -304,13 +310,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 
 // Scale group g (steps tg .. tg+SCG-1) into scale slot `ss` (waves w < NSD
-// copy 1 KB each).
+// copy 1 KB each; ssr: the scale buffer of the wave's operand).
 template <class C>
-__device__ __forceinline__ void issue_scales(uint8_t* ss, __amdgpu_buffer_rsrc_t wsr, const Plan<C>& P,
+__device__ __forceinline__ void issue_scales(uint8_t* ss, __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P,
                                              int tg, bool live) {
   const int wave = wave_id();
   const int go = (live && wave < C::NSD) ? 1 : 0;
-  dma16_if(uniform(go), wsr, P.s_base + (uint32_t)tg * P.s_step, lds_addr(ss + wave * 1024));
+  dma16_if(uniform(go), ssr, P.s_base + (uint32_t)tg * P.s_step, lds_addr(ss + wave * 1024));
 }
 
 // Fragments and raw scale dwords of the stage in data slot `sb`, whose step is
@@ -347,24 +353,27 @@ __device__ __forceinline__ void read_stage(const uint8_t* sb, const uint8_t* ss,
       F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
-  const uint32_t* sx = reinterpret_cast<const uint32_t*>(ss) + u * (C::BM + C::BN);
+  const uint32_t* sx = reinterpret_cast<const uint32_t*>(ss) + u * C::BM;
+  const uint32_t* sy = reinterpret_cast<const uint32_t*>(ss) + SCG * C::BM + u * C::BN;
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) xs[i] = sx[wm * C::WTM + i * 32 + r32];
 #pragma unroll
-  for (int j = 0; j < C::FN; ++j) ws[j] = sx[C::BM + wn * C::WTN + j * 32 + r32];
+  for (int j = 0; j < C::FN; ++j) ws[j] = sy[wn * C::WTN + j * 32 + r32];
 }
 
 // Move the scale byte of the lane's 32-element block of stage st (block
 // 2 st + hsel: byte 2 (st & 1) + hsel of the step's dword) to byte 0, where
-// op_sel 0 reads it; blocks outside [lo, hi) get the neutral scale 127, so
-// zero-filled data never meets a NaN scale byte.
+// op_sel 0 reads it; blocks wholly outside [lo, hi) get the neutral scale
+// 127, so zero-filled data never meets a NaN scale byte.  A block that only
+// partly overlaps [lo, hi) (a bound that is not a multiple of 32) keeps its
+// scale: its in-range elements are real data.
 template <class C>
 __device__ __forceinline__ void finish_scales(uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN], int st, int lo,
                                               int hi) {
   const int hsel = (threadIdx.x % kWave) >> 5;
   const int sh = 8 * hsel + 16 * (st & 1);
   const int k = st * BKS + 32 * hsel;
-  const bool out = k < lo || k >= hi;
+  const bool out = k + 32 <= lo || k >= hi;
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) xs[i] = out ? 127u : (xs[i] >> sh);
 #pragma unroll
@@ -425,7 +434,7 @@ __device__ __forceinline__ void interleave_step() {
 // (s0 is the ring's first stage, even, in slot 0; t0 = s0 / 2 its step.)
 template <class C>
 __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, const Operand& W,
-                                           __amdgpu_buffer_rsrc_t wsr, const Plan<C>& P, int s0, int r,
+                                           __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P, int s0, int r,
                                            int lo, int hi, Frags<C>& Fc, uint32_t (&xc)[C::FM],
                                            uint32_t (&wc)[C::FN], Frags<C>& Fn, uint32_t (&xn)[C::FM],
                                            uint32_t (&wn)[C::FN], v16f (&acc)[C::FM][C::FN]) {
@@ -451,7 +460,7 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   // so the drain after the last stage waits for no memory read)
   const int tg = s0 / 2 + (rn / SPG + 1) * SCG;
   const bool opens = rn % SPG == 0 && tg * STEP < hi;
-  issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, wsr, P, tg, opens);
+  issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, ssr, P, tg, opens);
   issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
   mfma_range<C, NE, NMMA>(Fc, xc, wc, acc);
   interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, C::LPS>();
@@ -470,17 +479,18 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
 // wholly outside [lo, hi): zero data, neutral scales, exactly zero added.
 template <class C>
 __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, const Operand& W,
-                                              __amdgpu_buffer_rsrc_t wsr, const ScaleSrc& xss,
-                                              const ScaleSrc& wss, int s0, int s1, int lo, int hi,
-                                              v16f (&acc)[C::FM][C::FN]) {
+                                              const ScaleSrc& xss, const ScaleSrc& wss, int s0, int s1,
+                                              int lo, int hi, v16f (&acc)[C::FM][C::FN]) {
   if (s0 >= s1) return;
   s0 &= ~1;
   Plan<C> P;
   make_plan<C>(P, X, W, xss, wss);
+  // the scale buffer this wave copies from (wave-uniform)
+  const __amdgpu_buffer_rsrc_t ssr = wave_id() < C::NSX ? xss.rsrc : wss.rsrc;
   // scale groups 0 and 1, then stages s0 .. s0+NS-1 (scales first: every
   // wait for a stage's copies then covers the scale copies issued before it)
-  issue_scales<C>(smem + C::SOFF, wsr, P, s0 / 2, true);
-  issue_scales<C>(smem + C::SOFF + C::SSLOT, wsr, P, s0 / 2 + SCG, true);
+  issue_scales<C>(smem + C::SOFF, ssr, P, s0 / 2, true);
+  issue_scales<C>(smem + C::SOFF + C::SSLOT, ssr, P, s0 / 2 + SCG, true);
 #pragma unroll
   for (int i = 0; i < C::NS; ++i) issue_stage<C>(smem + i * C::STAGE, X, W, P, s0 + i, lo, hi);
   MXGG_WAIT_VM((C::NS - 1) * C::LPS);
@@ -493,12 +503,101 @@ __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, c
   const int n = s1 - s0;
 #pragma nounroll
   for (int r = 0; r < n; r += 2) {
-    ring_stage<C>(smem, X, W, wsr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-    ring_stage<C>(smem, X, W, wsr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+    ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
   }
   // copies past the last stage (zero fills, scale groups) may still be
   // writing LDS: drain them before the LDS is reused or released
   MXGG_WAIT_VM(0);
+}
+
+// The in-range elements of the 16-element chunk at cs (a multiple of 16)
+// that straddles a bound of the reduction range [lo, hi).  The ring copies
+// whole chunks only, so a bound that is not a multiple of 16 leaves these
+// out; they are added here as one more 64-element MFMA step whose fragments
+// are loaded into registers, every element outside [lo, hi) and every other
+// chunk of the step zero.  MFMA operand layout (the one read_stage builds):
+// lane half h holds elements 16h .. 16h+15 of the step in dwords 0-3 and
+// 32+16h .. 32+16h+15 in dwords 4-7, and supplies the scale of the step's
+// block h (elements 32h .. 32h+31).  e4m3 on both sides (the weight
+// gradient's operands).
+template <class C>
+__device__ __forceinline__ void edge_chunk(const Operand& X, const Operand& W, const ScaleSrc& xss,
+                                           const ScaleSrc& wss, int cs, int lo, int hi,
+                                           v16f (&acc)[C::FM][C::FN]) {
+  static_assert(!C::F4, "edge chunks: e4m3 operands only");
+  const int wave = wave_id();
+  const int lane = threadIdx.x % kWave;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int h = lane >> 5, r32 = lane & 31;
+  const int kb = cs & ~(BKS - 1);                  // the step holding the chunk
+  const int ci = (cs - kb) >> 4;                   // chunk of the step: half (ci & 1), dwords 4 (ci >> 1) ..
+  const bool mine = h == (ci & 1);
+  // bytes b of the chunk with lo <= cs + b < hi
+  uint32_t mk[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int k = cs + 4 * d + b;
+      m |= (k >= lo && k < hi) ? (0xffu << (8 * b)) : 0u;
+    }
+    mk[d] = mine ? m : 0u;
+  }
+  Frags<C> F;
+  uint32_t xs[C::FM], ws[C::FN];
+  const int t = kb / STEP;
+  const int blk = (kb / 32 + h) & 3;               // byte of the lane's block in the step's dword
+  const bool live = kb + 32 * h < hi && kb + 32 * h + 32 > lo;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+    const uint32_t row = (uint32_t)(wm * C::WTM + i * 32 + r32);
+    const v4i v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(X.data, row * X.ld + cs, 0, 0));
+    v8i f = (v8i){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int w = v[d] & (int)mk[d];
+      if (ci >> 1) f[4 + d] = w; else f[d] = w;
+    }
+    F.b[i] = f;
+    const uint32_t s = __builtin_amdgcn_raw_buffer_load_b32(xss.rsrc, ((uint32_t)t * xss.rows + xss.row0 + row) * 4u, 0, 0);
+    xs[i] = live ? (s >> (8 * blk)) & 0xffu : 127u;
+  }
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const uint32_t row = (uint32_t)(wn * C::WTN + j * 32 + r32);
+    const v4i v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(W.data, row * W.ld + cs, 0, 0));
+    v8i f = (v8i){0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int w = v[d] & (int)mk[d];
+      if (ci >> 1) f[4 + d] = w; else f[d] = w;
+    }
+    F.a[j] = f;
+    const uint32_t s = __builtin_amdgcn_raw_buffer_load_b32(wss.rsrc, ((uint32_t)t * wss.rows + wss.row0 + row) * 4u, 0, 0);
+    ws[j] = live ? (s >> (8 * blk)) & 0xffu : 127u;
+  }
+  mfma_range<C, 0, C::FM * C::FN>(F, xs, ws, acc);
+  hold(F, xs, ws);
+  // What follows (a second edge step, the epilogue) may reuse these operand
+  // registers at once; the compiler does not count the scale operands as
+  // in-flight MFMA reads, so give the last MFMA time to read them.
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#endif
+}
+
+// Edge chunks of [lo, hi) (see edge_chunk): the chunk holding lo when lo is
+// not a multiple of 16, and the one holding hi when hi is not (once when
+// they are the same chunk).
+template <class C>
+__device__ __forceinline__ void edge_chunks(const Operand& X, const Operand& W, const ScaleSrc& xss,
+                                            const ScaleSrc& wss, int lo, int hi, v16f (&acc)[C::FM][C::FN]) {
+  if (hi <= lo) return;
+  const int clo = lo & ~15, chi = hi & ~15;
+  if (lo & 15) edge_chunk<C>(X, W, xss, wss, clo, lo, hi, acc);
+  if ((hi & 15) && !((lo & 15) && chi == clo)) edge_chunk<C>(X, W, xss, wss, chi, lo, hi, acc);
 }
 
 // Store 4 consecutive output columns c .. c+3 of row r (those below `cols`)
@@ -784,7 +883,8 @@ __global__ __launch_bounds__(256) void scale_relayout_kernel(ScaleJobs js) {
 struct FwdParams {
   const uint8_t* a; int64_t lda;
   const uint8_t* b; int64_t ldb_n; int64_t ldb_e;
-  const uint8_t* ws; uint32_t ws_bytes;     // re-laid scales: A [T][M], then B [E][T][N]
+  const uint8_t* as; uint32_t as_bytes;     // A scales, step-major [T][M] dwords (T = cdiv(K, 128))
+  const uint8_t* bs; uint32_t bs_expert;    // B scales, step-major [E][T][N] dwords; bytes per expert
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype; int64_t ldo;
   int grid_n; int group_m; int xcd;
@@ -862,10 +962,8 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
   X.data = make_rsrc(p.a + row0 * p.lda, (uint32_t)rows * X.ld);
   W.ld = (uint32_t)p.ldb_n;
   W.data = make_rsrc(p.b + (int64_t)tl.expert * p.ldb_e + n0 * p.ldb_n, (uint32_t)cols * W.ld);
-  const uint32_t T = (uint32_t)((p.K + STEP - 1) / STEP);
-  const ScaleSrc xs{0u, (uint32_t)p.M, (uint32_t)row0};
-  const ScaleSrc ws{4u * T * ((uint32_t)p.M + (uint32_t)tl.expert * (uint32_t)p.N), (uint32_t)p.N, (uint32_t)n0};
-  const __amdgpu_buffer_rsrc_t wsr = make_rsrc(p.ws, p.ws_bytes);
+  const ScaleSrc xs{make_rsrc(p.as, p.as_bytes), (uint32_t)p.M, (uint32_t)row0};
+  const ScaleSrc ws{make_rsrc(p.bs + (int64_t)tl.expert * p.bs_expert, p.bs_expert), (uint32_t)p.N, (uint32_t)n0};
 
   v16f acc[C::FM][C::FN];
 #pragma unroll
@@ -876,13 +974,13 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
   const int K = (int)p.K;
   if constexpr (PIECES) {
     int a, b;
-    split_range(0, (int)T, piece, S, a, b);
+    split_range(0, (int)((p.K + STEP - 1) / STEP), piece, S, a, b);
     const int lo = STEP * a;
     const int hi = STEP * b < K ? STEP * b : K;
-    ring_mainloop<C>(smem, X, W, wsr, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
+    ring_mainloop<C>(smem, X, W, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
     store_partial<C>(acc, p.part + (int64_t)slot * (C::BM * C::BN));
   } else {
-    ring_mainloop<C>(smem, X, W, wsr, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
+    ring_mainloop<C>(smem, X, W, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
     if constexpr (EPI == kEpiBf16) {
       store_tile_lds<C, true>(acc, smem, p.out + (row0 * p.ldo + n0) * 2, p.ldo, rows, cols);
     } else {
@@ -1037,7 +1135,8 @@ __global__ __launch_bounds__(256) void fwd_reduce_kernel(FwdParams p) {
 struct WgradParams {
   const uint8_t* go; int64_t ld_go;
   const uint8_t* ia; int64_t ld_ia;
-  const uint8_t* ws; uint32_t ws_bytes;     // re-laid scales: GO [T][N], then IA [T][K]
+  const uint8_t* gs; uint32_t gs_bytes;     // GO scales, step-major [T][N] dwords (T = cdiv(M, 128))
+  const uint8_t* is; uint32_t is_bytes;     // IA scales, step-major [T][K] dwords
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype;
   int tiles_n; int tiles_k;
@@ -1260,10 +1359,8 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   X.data = make_rsrc(p.go + n0 * p.ld_go, (uint32_t)rows * X.ld);
   W.ld = (uint32_t)p.ld_ia;
   W.data = make_rsrc(p.ia + k0 * p.ld_ia, (uint32_t)cols * W.ld);
-  const uint32_t T = (uint32_t)((p.M + STEP - 1) / STEP);
-  const ScaleSrc xs{0u, (uint32_t)p.N, (uint32_t)n0};
-  const ScaleSrc ws{4u * T * (uint32_t)p.N, (uint32_t)p.K, (uint32_t)k0};
-  const __amdgpu_buffer_rsrc_t wsr = make_rsrc(p.ws, p.ws_bytes);
+  const ScaleSrc xs{make_rsrc(p.gs, p.gs_bytes), (uint32_t)p.N, (uint32_t)n0};
+  const ScaleSrc ws{make_rsrc(p.is, p.is_bytes), (uint32_t)p.K, (uint32_t)k0};
 
   v16f acc[C::FM][C::FN];
 #pragma unroll
@@ -1271,7 +1368,10 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 
-  if (hi > lo) ring_mainloop<C>(smem, X, W, wsr, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
+  if (hi > lo) ring_mainloop<C>(smem, X, W, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
+  // group bounds that are not multiples of 16 (any offsets are accepted, as
+  // in the reference): the straddling chunks' in-group tokens
+  if ((lo | hi) & 15) edge_chunks<C>(X, W, xs, ws, lo, hi, acc);
 
   if constexpr (PIECES) {
     store_partial<C>(acc, p.part + (int64_t)blockIdx.x * (C::BM * C::BN));
@@ -1307,47 +1407,55 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// routing table / schedule (test hooks exposing the in-kernel device code)
+// routing table / tile order: test hooks that run the GEMMs' own device code
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(64) void routing_kernel(const int32_t* offs, int E, int BM,
-                                                     int grid_m_ub, int32_t* out) {
-  // one wave; hist / start rows then the pid map
+// The reference's routing buffer [hist E | start E | total | map grid_m_ub]
+// (kernels/forward.py:320-354), built with the lookup the GEMMs run: with
+// one column tile and bands of one m-block, route_tile's order is the
+// reference's m-block order, so tile t is m-block t of the map.  One wave.
+__global__ __launch_bounds__(64) void routing_kernel(const int32_t* offs, int E, int BM, int grid_m_ub,
+                                                     int32_t* out) {
   for (int e = threadIdx.x; e < E; e += kWave) {
     int prev = e > 0 ? offs[e - 1] : 0;
     out[e] = offs[e] - prev;
     out[E + e] = prev;
   }
-  const int total = route_total(offs, E, BM);
+  WaveGroups wg{0, 0, 0, 0, 0};
+  int total;
+  if (E <= kWave) {
+    wg = load_groups(offs, E, BM);
+    total = wg.total;
+  } else {
+    total = route_total(offs, E, BM);
+  }
   if (threadIdx.x == 0) out[2 * E] = total;
-  for (int base = 0; base < grid_m_ub; base += kWave) {
-    // every lane resolves a different pid; route_find is wave-collective, so
-    // loop over the wave's pids one at a time
-    for (int k = 0; k < kWave && base + k < grid_m_ub; ++k) {
-      int pid = base + k;
-      int v = -1;
-      if (pid < total) {
-        TileRoute r = route_find(offs, E, BM, pid);
-        if (r.expert >= 0) v = (r.block << 16) | r.expert;
-      }
-      if (threadIdx.x == 0) out[2 * E + 1 + pid] = v;
-    }
+  for (int pid = 0; pid < grid_m_ub; ++pid) {
+    int pn;
+    const TileRoute r = E <= kWave ? route_tile(wg, E, BM, 1, 1, pid, pn) : route_tile(offs, E, BM, 1, 1, pid, pn);
+    if (threadIdx.x == 0) out[2 * E + 1 + pid] = r.expert >= 0 ? (r.block << 16) | r.expert : -1;
   }
 }
 
-__global__ __launch_bounds__(64) void schedule_kernel(const int32_t* offs, int E, int BM,
-                                                      int grid_n, int group_m, int xcd,
-                                                      int programs, int32_t* out) {
-  const int total_m = route_total(offs, E, BM);
-  const int tiles = total_m * grid_n;
-  for (int pid = threadIdx.x; pid < programs; pid += kWave) {
-    int pm = -1, pn = -1;
-    if (pid < tiles) {
-      int t = xcd > 1 ? xcd_swizzle(pid, tiles, xcd) : pid;
-      pid_grid(t, total_m, grid_n, group_m, pm, pn);
+// The forward kernels' tile order: for every program id of the whole-tile
+// grid, the tile fwd_tile gives it (the XCD swizzle, then the expert-aligned
+// bands of route_tile), as 5 int32s (expert, row0, rows, n0, cols), or -1s
+// past the tiles.  One wave per workgroup, programs strided over the grid.
+template <class C>
+__global__ __launch_bounds__(64) void schedule_kernel(FwdParams p, int programs, int32_t* out) {
+  WaveGroups wg;
+  const int tiles = fwd_groups<C>(p, wg) * p.grid_n;
+  for (int pid = blockIdx.x; pid < programs; pid += gridDim.x) {
+    FwdTile tl;
+    const bool ok = pid < tiles && fwd_tile<C>(p, pid, tiles, wg, tl);
+    if (threadIdx.x < 5) {
+      int v = -1;
+      if (ok) {
+        const int64_t f[5] = {tl.expert, tl.row0, tl.rows, tl.n0, tl.cols};
+        v = (int)f[threadIdx.x];
+      }
+      out[5 * (int64_t)pid + threadIdx.x] = v;
     }
-    out[2 * pid] = pm;
-    out[2 * pid + 1] = pn;
   }
 }
 
@@ -1561,14 +1669,32 @@ extern "C" int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t
                                   void* stream) {
   clear_error();
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: E=%d out of range", E);
-  if (block_m <= 0 || block_n <= 0 || group_m <= 0 || xcd_swizzle <= 0)
-    return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: block sizes, group_m and xcd_swizzle must be positive");
+  if (M < 0 || N < 0 || M > INT32_MAX || N > INT32_MAX)
+    return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: M, N out of range");
+  if (group_m <= 0 || xcd_swizzle <= 0)
+    return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: group_m and xcd_swizzle must be positive");
+  if (!((block_m == 256 && block_n == 256) || (block_m == 128 && block_n == 128)))
+    return fail(MXGG_ERR_UNSUPPORTED, "tile_schedule: tile %dx%d not built", block_m, block_n);
   const int64_t programs = mxgg_schedule_programs(E, M, N, block_m, block_n);
-  if (programs > INT32_MAX) return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: too many programs");
+  if (programs > INT32_MAX / 5) return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: too many programs");
   if (!offs || !out) return fail(MXGG_ERR_INVALID_ARG, "tile_schedule: null pointer");
   if (int rc = require_device()) return rc;
-  hipLaunchKernelGGL(schedule_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, offs, E, block_m,
-                     (int)cdiv(N, block_n), group_m, xcd_swizzle, (int)programs, out);
+  if (programs == 0) return MXGG_OK;
+  FwdParams p{};
+  p.offs = offs;
+  p.E = E;
+  p.M = M;
+  p.N = N;
+  p.grid_n = (int)cdiv(N, block_n);
+  p.group_m = group_m;
+  p.xcd = xcd_swizzle;
+  const unsigned grid = (unsigned)(programs < 1024 ? programs : 1024);
+  if (block_m == 256)
+    hipLaunchKernelGGL(schedule_kernel<CfgF8_256>, dim3(grid), dim3(64), 0, (hipStream_t)stream, p, (int)programs,
+                       out);
+  else
+    hipLaunchKernelGGL(schedule_kernel<CfgF8_128>, dim3(grid), dim3(64), 0, (hipStream_t)stream, p, (int)programs,
+                       out);
   return launch_status("tile_schedule");
 }
 
@@ -1654,7 +1780,8 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   const size_t part_off = align256(need);
   float* part = c.split && ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
   const size_t part_bytes = part ? ws_bytes - part_off : 0;
-  FwdParams p{A, lda, B, ldb_n, ldb_e, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
+  FwdParams p{A, lda, B, ldb_n, ldb_e, (const uint8_t*)workspace, (uint32_t)(4 * T * M),
+              (const uint8_t*)(wsd + T * M), (uint32_t)(4 * T * N), offs, E, M, N, K,
               (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0};
   if (b_fmt == MXGG_FMT_E2M1)
     return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, part_bytes, st);
@@ -1739,7 +1866,8 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   }
   const size_t part_off = align256(need);
   float* part = ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
-  WgradParams p{go_t, ld_go, ia_t, ld_ia, (const uint8_t*)workspace, (uint32_t)need, offs, E, M, N, K,
+  WgradParams p{go_t, ld_go, ia_t, ld_ia, (const uint8_t*)workspace, (uint32_t)(4 * T * N),
+                (const uint8_t*)(wsd + T * N), (uint32_t)(4 * T * K), offs, E, M, N, K,
                 (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0, 0, 0, 0};
   const int64_t tiles = (int64_t)E * p.tiles_n * p.tiles_k;
   if (tiles > INT32_MAX / 2) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");

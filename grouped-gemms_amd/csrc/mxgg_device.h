@@ -194,48 +194,13 @@ struct TileRoute {
   int rows;      // valid rows of this tile (<= BM)
 };
 
-// Owner of M-tile `pid_m` (0 <= pid_m < route_total).  Wave-uniform.
-__device__ __forceinline__ TileRoute route_find(const int32_t* __restrict__ offs, int E, int BM,
-                                                int pid_m) {
-  const int lane = threadIdx.x & (kWave - 1);
-  TileRoute r{-1, 0, 0, 0};
-  int carry = 0;
-  for (int base = 0; base < E; base += kWave) {
-    int e = base + lane;
-    int nb = 0, h = 0, prev = 0;
-    if (e < E) {
-      int end = offs[e];
-      prev = e > 0 ? offs[e - 1] : 0;
-      h = end - prev;
-      nb = h > 0 ? (h + BM - 1) / BM : 0;
-    }
-    int incl = wave_incl_scan(nb) + carry;
-    int excl = incl - nb;
-    bool own = (e < E) && (nb > 0) && (pid_m >= excl) && (pid_m < incl);
-    unsigned long long m = __ballot(own);
-    if (m) {
-      int src = __ffsll((long long)m) - 1;
-      int ex = lane_value(excl, src);
-      r.expert = uniform(base + src);
-      r.block = pid_m - ex;
-      r.start = lane_value(prev, src);
-      int hh = lane_value(h, src);
-      int rem = hh - r.block * BM;
-      r.rows = rem < BM ? rem : BM;
-      return r;
-    }
-    carry = lane_value(incl, kWave - 1);
-  }
-  return r;
-}
-
 // Expert-aligned tile order used by the GEMMs: the tiles of group e (its
 // cdiv(hist[e], BM) m-blocks x grid_n column tiles) are contiguous in the
 // logical order, groups in order; inside a group the m-blocks form bands of
 // at most group_m (balanced: nbands = cdiv(blocks, group_m), height
 // cdiv(blocks, nbands), the last band shorter), column-major inside a band.
 // Unlike the reference's GROUP_M bands over the global m-block index
-// (kernels/forward.py:38-51, `pid_grid` below), no band mixes two groups, so
+// (kernels/forward.py:38-51), no band mixes two groups, so
 // the tiles in flight on an XCD read one group's weights.  Returns the owner
 // of logical tile t (0 <= t < total blocks x grid_n) and its column tile pn;
 // expert < 0 past the end.  Wave-uniform.
@@ -331,22 +296,6 @@ __device__ __forceinline__ int xcd_swizzle(int pid, int domain, int X) {
   const int q = pid / X;
   const int g = pid - q * X;
   return g * per + (g < extra ? g : extra) + q;
-}
-
-// GROUP_M band ordering (kernels/forward.py:38-51).
-__device__ __forceinline__ void pid_grid(int pid, int num_m, int num_n, int group_m, int& pm,
-                                         int& pn) {
-  if (group_m <= 1) {
-    pm = pid / num_n;
-    pn = pid % num_n;
-    return;
-  }
-  int in_group = group_m * num_n;
-  int gid = pid / in_group;
-  int first = gid * group_m;
-  int size = num_m - first < group_m ? num_m - first : group_m;
-  pm = first + pid % size;
-  pn = (pid % in_group) / size;
 }
 
 }  // namespace mxgg

@@ -36,7 +36,9 @@ def triton_mxfp8_wgrad(
         go_scale: ``(N, M//32)`` e8m0.
         ia_t: ``(K, M)`` float8_e4m3fn, input activations quantized along M.
         ia_scale: ``(K, M//32)`` e8m0.
-        group_end_offsets: ``(E,)`` int32 cumulative token counts, multiples of 32.
+        group_end_offsets: ``(E,)`` int32 cumulative token counts (any
+            nondecreasing values up to M; a 32-token scale block shared by
+            two groups scales the tokens of both, as in the reference).
         BLOCK_N / BLOCK_K / BLOCK_M / num_warps / num_stages: accepted for
             signature compatibility; the HIP kernel uses its own tiling.
 

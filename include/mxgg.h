@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_VERSION 2002 /* major*1000 + minor */
+#define MXGG_VERSION 3000 /* major*1000 + minor */
 
 /* status codes */
 #define MXGG_OK 0
@@ -109,19 +109,26 @@ int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t batch, int64_t
  * [hist E | start E | total 1 | map grid_m_ub] (int32), where
  * grid_m_ub = cdiv(M, block_m) + max(E-1, 0) and map[p] = (block << 16) | e or -1.
  * Replaces `_build_expt_data` / `_expt_data_kernel` (kernels/forward.py:296-365).
- * The GEMM entry points compute the same table inside the kernel; this entry
- * point exposes that device code.  out must hold mxgg_routing_words() int32s.
+ * The GEMMs build no such buffer: every workgroup looks its tile up from offs.
+ * This test hook fills the reference's buffer with that same lookup
+ * (route_tile with one column tile and bands of one m-block, whose order is
+ * the reference's m-block order).  out must hold mxgg_routing_words() int32s.
  */
 int64_t mxgg_routing_words(int E, int64_t M, int block_m);
 int mxgg_build_routing(const int32_t* offs, int E, int64_t M, int block_m, int32_t* out,
                        void* stream);
 
 /*
- * Tile schedule of the grouped GEMM: for every program id of the launch grid
- * (grid_m_ub * cdiv(N, block_n) programs) writes (pid_m, pid_n) or (-1, -1)
- * for programs that exit, after the XCD swizzle and GROUP_M ordering.
- * Replaces `_xcd_swizzle` / `_pid_grid` and their use in the GEMM
- * (kernels/forward.py:31-51, 111-127).  out holds 2 * programs int32s.
+ * Tile order of the forward / dgrad GEMM (test hook): for every program id p
+ * of the whole-tile launch grid (mxgg_schedule_programs() programs) writes
+ * the tile the kernel computes there, out[5p .. 5p+4] = (expert, row0, rows,
+ * n0, cols), or five -1s for programs that exit.  It runs the kernel's own
+ * routing code: the XCD swizzle of the reference (kernels/forward.py:31-36),
+ * then expert-aligned GROUP_M bands -- the tiles of each group contiguous,
+ * cut into bands of at most group_m m-blocks, column-major inside a band --
+ * in place of the reference's bands over the global m-block index
+ * (kernels/forward.py:38-51, 111-127).  block_m x block_n must be a built
+ * tile (256 x 256 or 128 x 128).
  */
 int64_t mxgg_schedule_programs(int E, int64_t M, int64_t N, int block_m, int block_n);
 int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t N, int block_m,
@@ -184,7 +191,10 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
  * store of bf16-rounded values whatever out_dtype is (backward.py:103, 214).
  *   go_t  (N, M) e4m3, row stride ld_go;   go_s (N, M/32), row stride ld_gos
  *   ia_t  (K, M) e4m3, row stride ld_ia;   ia_s (K, M/32), row stride ld_ias
- *   offs  (E,) int32 cumulative group ends, multiples of 32, offs[E-1] <= M
+ *   offs  (E,) int32 cumulative group ends, nondecreasing, offs[E-1] <= M.
+ *         Any values: as in the reference (token masks by group, scales by
+ *         token / 32), a 32-token scale block shared by two groups scales the
+ *         tokens of both.
  *   out   (E, N, K) of out_dtype (BF16 or F32), contiguous
  *   workspace / ws_bytes: device scratch, need not be initialised.  Required:
  *         4 * ceil(M/128) * (N + K) bytes (the scales re-laid step-major);

@@ -313,6 +313,66 @@ def tile_schedule(offs, M: int, N: int, block_m: int, block_n: int, group_m: int
     return np.array(out, dtype=np.int32).reshape(-1, 2)
 
 
+def band_tile(blocks: int, grid_n: int, group_m: int, local: int):
+    """(m-block, column tile) of tile ``local`` of one group in the build's
+    expert-aligned band order.
+
+    Not the reference's order: kernels/forward.py:38-51 cuts GROUP_M bands
+    from the global m-block index, so a band can span two experts.  The build
+    keeps each group's ``blocks x grid_n`` tiles contiguous and cuts the
+    group's m-blocks into ``cdiv(blocks, group_m)`` balanced bands (height
+    ``cdiv(blocks, nbands)``, the last band shorter), column-major inside a
+    band.
+    """
+    g = max(int(group_m), 1)
+    nbands = -(-blocks // g)
+    bh = -(-blocks // nbands)
+    b = min(local // (bh * grid_n), nbands - 1)
+    in_band = local - b * bh * grid_n
+    hb = blocks - b * bh if b == nbands - 1 else bh
+    col = in_band // hb
+    return b * bh + (in_band - col * hb), col
+
+
+def fwd_tile_order(offs, M: int, N: int, block_m: int, block_n: int, group_m: int, xcd: int) -> np.ndarray:
+    """The build's forward tile order: program id -> ``(expert, row0, rows,
+    n0, cols)``, or five -1s for programs that compute nothing.
+
+    Grid = ``(cdiv(M, BM) + E - 1) * cdiv(N, BN)`` programs, as the
+    reference's (kernels/forward.py:347, 111-127).  A program id below the
+    tile count is mapped by the XCD swizzle (kernels/forward.py:31-36) over
+    the tile domain, then to the group whose tiles hold that index (groups in
+    order, each group's tiles contiguous) and through ``band_tile``.  A tile
+    holds rows ``row0 = offs[e-1] + block*BM`` up to the group's end, BM at
+    most, and none at or past M.
+    """
+    offs = [int(v) for v in np.asarray(offs).reshape(-1)]
+    E = len(offs)
+    groups = []
+    prev = 0
+    for off in offs:
+        h = off - prev
+        groups.append((prev, h, -(-h // block_m) if h > 0 else 0))
+        prev = off
+    grid_n = -(-N // block_n)
+    tiles = sum(nb for _, _, nb in groups) * grid_n
+    programs = (-(-M // block_m) + max(E - 1, 0)) * grid_n
+    out = np.full((programs, 5), -1, dtype=np.int64)
+    for pid in range(min(programs, tiles)):
+        t = xcd_swizzle(pid, tiles, xcd) if xcd > 1 else pid
+        base = 0
+        for e, (start, h, nb) in enumerate(groups):
+            if nb and base <= t < base + nb * grid_n:
+                block, col = band_tile(nb, grid_n, group_m, t - base)
+                row0 = start + block * block_m
+                rows = min(M - row0, h - block * block_m, block_m)
+                if rows > 0:
+                    out[pid] = (e, row0, rows, col * block_n, min(N - col * block_n, block_n))
+                break
+            base += nb * grid_n
+    return out
+
+
 # ----------------------------------------------------------------------------
 # grouped GEMMs (dequantize -> per-group matmul)
 # ----------------------------------------------------------------------------
@@ -412,6 +472,10 @@ PINNING = {
     "generate_jagged_offs": "invariants (sorted, distinct, multiples, last=M) and errors",
     "routing_table": "hand-derived KAT (E=4, offs=[96,352,640,1024], BM=128) plus brute force",
     "xcd_swizzle/pid_grid": "KAT (D=10, X=8) and bijection over many domains",
+    "band_tile/fwd_tile_order": "hand-derived KAT (E=4, offs=[96,352,640,1024], BM=BN=128, N=256, "
+                                "GROUP_M=2); brute force: every output element of every group covered "
+                                "by exactly one program, none past offs[-1]; equal to the reference's "
+                                "routing map (routing_table) with one column tile and bands of one block",
     "grouped_mm/wgrad": "closed forms: E=1 equals a plain matmul; unit scales reduce to fp8 matmul; "
                         "zero inputs give zeros; SQNR vs the unquantized product",
 }

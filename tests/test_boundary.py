@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.mxgg_version() == 2002
+    assert lib.mxgg_version() == 3000
     assert isinstance(lib.mxgg_last_error_string(), bytes)
 
 

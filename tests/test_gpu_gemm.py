@@ -317,6 +317,26 @@ def test_wgrad_fp32_out_is_bf16_rounded(gpu):
     _assert_close(f32(out), ref)
 
 
+@pytest.mark.parametrize("M,offs", [(1024, [16, 48, 1000, 1024]),          # 16- but not 32-aligned bounds
+                                    (1024, [7, 100, 333, 1024]),           # bounds off the 16 grid
+                                    (1024, [3, 10, 10, 517, 1024]),        # two bounds in one 16-chunk, empty group
+                                    (1024, [0, 1, 1023, 1024]),            # one-token groups at both ends
+                                    (8192, [4100, 8190])])                 # long groups (split plan), tail unrouted
+def test_wgrad_any_offsets(gpu, M, offs):
+    """Group bounds need not be multiples of 32 (the reference masks tokens by
+    group and indexes scales by token // 32, kernels/backward.py:67-98): a
+    32-token scale block shared by two groups scales both groups' tokens."""
+    E, N, K = len(offs), 320, 288
+    out, ref, _, _ = _wgrad_case(E, M, N, K, offs, gpu, seed=len(offs) + M)
+    o = f32(out)
+    prev = 0
+    for e, end in enumerate(offs):
+        if end == prev:
+            assert (o[e] == 0).all()
+        prev = end
+    _assert_close(o, ref)
+
+
 # ---------------------------------------------------------------- routing / schedule
 
 def test_routing_table_kat(gpu):
@@ -348,16 +368,35 @@ def test_routing_matches_oracle(gpu, E, M, BM):
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("E,M,N,BM,BN,GM,X", [(8, 16640, 8192, 256, 256, 8, 8), (1, 16640, 2048, 128, 128, 16, 4),
-                                              (3, 1000, 640, 128, 128, 4, 8), (5, 4096, 1024, 256, 256, 1, 1)])
-def test_tile_schedule_matches_oracle(gpu, E, M, N, BM, BN, GM, X):
+def _order_offs(case):
+    """Offsets for the tile-order test: seeded jagged groups, or (for
+    'many') 80 groups with a fifth of them empty and sizes off the 32 grid."""
+    kind, E, M = case
+    if kind == "jagged":
+        return seeded_offs(E, M, seed=E * 31 + M)
+    rng = np.random.default_rng(E)
+    sizes = rng.integers(1, 6, size=E) * 37
+    sizes[rng.choice(E, E // 5, replace=False)] = 0
+    return np.cumsum(sizes).astype(np.int32)
+
+
+@pytest.mark.parametrize("case", [("jagged", 8, 16640), ("jagged", 1, 16640), ("jagged", 3, 1024), ("many", 80, 9000)])
+@pytest.mark.parametrize("BM", [256, 128])
+@pytest.mark.parametrize("GM,X", [(1, 1), (3, 8), (12, 8), (12, 1)])
+def test_tile_schedule_matches_oracle(gpu, case, BM, GM, X):
+    """The forward kernel's own tile lookup (fwd_tile: XCD swizzle, then
+    expert-aligned bands), run for every program of the launch grid, equals
+    the oracle's restatement, which the CPU tests pin to cover every output
+    element exactly once."""
     from kernels import _lib
     lib = _lib.load()
-    offs = seeded_offs(E, M - M % 32, seed=N) if M % 32 == 0 else np.array([100, 500, 1000][:E], np.int32)
-    progs = lib.mxgg_schedule_programs(E, M, N, BM, BN)
-    out = torch.empty((2 * progs,), dtype=torch.int32, device=gpu)
-    _lib.check(lib.mxgg_tile_schedule(torch.tensor(offs, device=gpu).data_ptr(), E, M, N, BM, BN, GM, X,
-                                      out.data_ptr(), torch.cuda.current_stream().cuda_stream))
-    torch.cuda.synchronize()
-    ref = O.tile_schedule(offs, M, N, BM, BN, GM, X)
-    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1, 2), ref)
+    offs = _order_offs(case)
+    E, M = len(offs), case[2]
+    for N in (2048, 700):
+        progs = lib.mxgg_schedule_programs(E, M, N, BM, BM)
+        out = torch.full((5 * progs,), -7, dtype=torch.int32, device=gpu)
+        _lib.check(lib.mxgg_tile_schedule(torch.tensor(offs, device=gpu).data_ptr(), E, M, N, BM, BM, GM, X,
+                                          out.data_ptr(), torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        ref = O.fwd_tile_order(offs, M, N, BM, BM, GM, X)
+        np.testing.assert_array_equal(out.cpu().numpy().reshape(-1, 5), ref)

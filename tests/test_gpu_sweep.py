@@ -1,0 +1,150 @@
+"""Full-size parity on every shape the benchmark measures (BASELINE configs 3
+and 4): the 36-shape sweep E in {1, 2, 4, 8}, M = 16640, N, K in {2048, 5120,
+8192}, as forward, dgrad and wgrad, with the bench's own offsets (the
+reference's draw: random.seed(123), generate_jagged_offs in config order;
+reference bench.py:113-122, 250-257).
+
+Per shape and direction:
+  * every group's output within rel-Frobenius 3e-3 of a GPU fp32 dequantize ->
+    matmul of the same quantized operands (north_star gate: 1e-2);
+  * every group at >= 27 dB SQNR against the fp32 product of the unquantized
+    bf16 operands (test_correctness.py:26; all three directions sit at
+    ~27.6 dB with these input distributions);
+  * the GPU reference itself pinned to the CPU oracle (oracle.grouped_mm /
+    oracle.wgrad, fp64) on a slice: 256 rows across a group boundary x 128
+    columns (forward, dgrad), or a 64 x 64 block of every group (wgrad).
+"""
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits_u8
+from oracle import mx_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+M_TOKENS = 16640
+SHAPES = [(e, n, k) for e in (1, 2, 4, 8) for n in (2048, 5120, 8192) for k in (2048, 5120, 8192)]
+REL_FRO_TIGHT = 3e-3
+SQNR_GATE = 27.0
+REF_PIN = 1e-4          # GPU fp32 reference vs oracle fp64, same quantized operands
+
+
+def _bench_offs():
+    r = random.Random(123)
+    return {s: O.generate_jagged_offs(s[0], M_TOKENS, 32, rng=r) for s in SHAPES}
+
+
+OFFS = _bench_offs()
+
+
+def _deq(q, s):
+    """e4m3 + e8m0 per-32 scales along the last dim -> fp32 (exact)."""
+    v = q.float().reshape(*q.shape[:-1], -1, 32)
+    return (v * torch.exp2(s.view(torch.uint8).float() - 127).unsqueeze(-1)).reshape(q.shape)
+
+
+def _gen(shape, std, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(shape, device=dev, generator=g) * std).to(torch.bfloat16)
+
+
+def _bounds(offs):
+    prev = 0
+    for e, end in enumerate(offs):
+        yield e, prev, int(end)
+        prev = int(end)
+
+
+def _check_group(out_g, ref_g, hp_g, what):
+    d = (out_g.float() - ref_g).norm().item()
+    r = ref_g.norm().item()
+    assert d <= REL_FRO_TIGHT * r, f"{what}: rel_fro {d / r:.3e}"
+    if hp_g is not None:
+        e = (out_g.float() - hp_g).norm().item()
+        sq = 20 * np.log10(hp_g.norm().item() / e)
+        assert sq >= SQNR_GATE, f"{what}: sqnr {sq:.2f} dB"
+
+
+def _nt_case(gpu, E, rows_n, red, offs, seed, what):
+    """out (M, rows_n) = X (M, red) @ W[g]^T (E, rows_n, red) per group: the
+    forward (rows_n = N, red = K) and dgrad (grad_out against W^T viewed
+    (E, K, N): rows_n = K, red = N) calls."""
+    import kernels
+    M = M_TOKENS
+    print(f"{what} E={E} M={M} out={rows_n} red={red} offs={list(offs)}", flush=True)
+    x = _gen((M, red), 1.0, seed, gpu)
+    w = _gen((E, rows_n, red), 0.02, seed + 1, gpu)
+    sx, qx = kernels.to_mx(x)
+    sw, qw = kernels.to_mx(w)
+    out = kernels.triton_mxfp8_grouped_mm(qx, qw, sx, sw, torch.tensor(offs, dtype=torch.int32, device=gpu))
+    xd, wd = _deq(qx, sx), _deq(qw, sw)
+    ref_slice = None
+    r0 = max(0, min(int(offs[0]) - 128, M - 256)) if E > 1 else 0
+    for e, lo, hi in _bounds(offs):
+        if hi <= lo:
+            continue
+        ref = xd[lo:hi] @ wd[e].t()
+        hp = x[lo:hi].float() @ w[e].float().t()
+        _check_group(out[lo:hi], ref, hp, f"{what} group {e}")
+        # rows r0 .. r0+255 of the fp32 reference, columns 0 .. 127
+        a, b = max(lo, r0), min(hi, r0 + 256)
+        if a < b:
+            if ref_slice is None:
+                ref_slice = torch.empty((256, 128), device=gpu)
+            ref_slice[a - r0:b - r0] = ref[a - lo:b - lo, :128]
+        del ref, hp
+    # pin the GPU reference (and the kernel) to the oracle on the slice
+    so = np.clip(np.asarray(offs, np.int64) - r0, 0, 256)
+    ora = O.grouped_mm(bits_u8(qx[r0:r0 + 256]), bits_u8(sx[r0:r0 + 256]),
+                       bits_u8(qw[:, :128]), bits_u8(sw[:, :128]), so)
+    g = ref_slice.double().cpu().numpy()
+    assert O.rel_fro(ora, g) <= REF_PIN
+    assert O.rel_fro(ora, out[r0:r0 + 256, :128].float().cpu().numpy()) <= REL_FRO_TIGHT
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"E{e}-N{n}-K{k}" for e, n, k in SHAPES])
+def test_sweep_fwd(gpu, shape):
+    E, N, K = shape
+    _nt_case(gpu, E, N, K, OFFS[shape], seed=E * 100 + N + K, what="fwd")
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"E{e}-N{n}-K{k}" for e, n, k in SHAPES])
+def test_sweep_dgrad(gpu, shape):
+    E, N, K = shape
+    _nt_case(gpu, E, K, N, OFFS[shape], seed=E * 100 + N + K + 7, what="dgrad")
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"E{e}-N{n}-K{k}" for e, n, k in SHAPES])
+def test_sweep_wgrad(gpu, shape):
+    """out[g] (N, K) = grad_out[g]^T @ A[g] over each group's tokens, from
+    the dim-1 quantized operands (scales per 32 tokens)."""
+    import kernels
+    E, N, K = shape
+    M = M_TOKENS
+    offs = OFFS[shape]
+    print(f"wgrad E={E} M={M} N={N} K={K} offs={list(offs)}", flush=True)
+    seed = E * 100 + N + K + 13
+    go = _gen((M, N), 1.0, seed, gpu)
+    ia = _gen((M, K), 1.0, seed + 1, gpu)
+    sg, qg = kernels.to_mx_dim0(go)          # (N, M)
+    si, qi = kernels.to_mx_dim0(ia)          # (K, M)
+    out = kernels.triton_mxfp8_wgrad(qg, sg, qi, si, torch.tensor(offs, dtype=torch.int32, device=gpu))
+    gd, idq = _deq(qg, sg), _deq(qi, si)
+    for e, lo, hi in _bounds(offs):
+        if hi <= lo:
+            assert (out[e] == 0).all()
+            continue
+        ref = gd[:, lo:hi] @ idq[:, lo:hi].t()
+        hp = go[lo:hi].float().t() @ ia[lo:hi].float()
+        _check_group(out[e], ref, hp, f"wgrad group {e}")
+        # pin: a 64 x 64 block of this group against the oracle
+        n0, k0 = (e * 64) % N, (e * 192) % K
+        ora = O.wgrad(bits_u8(qg[n0:n0 + 64]), bits_u8(sg[n0:n0 + 64]),
+                      bits_u8(qi[k0:k0 + 64]), bits_u8(si[k0:k0 + 64]), offs)[e]
+        assert O.rel_fro(ora, ref[n0:n0 + 64, k0:k0 + 64].double().cpu().numpy()) <= REF_PIN
+        assert O.rel_fro(ora, out[e, n0:n0 + 64, k0:k0 + 64].float().cpu().numpy()) <= REL_FRO_TIGHT
+        del ref, hp

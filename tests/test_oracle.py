@@ -289,6 +289,72 @@ def test_tile_schedule_covers_every_tile_once():
     assert len({tuple(r) for r in live.tolist()}) == len(live)
 
 
+def test_fwd_tile_order_kat():
+    """Hand-derived from the band rule: groups of 1, 2, 3, 3 m-blocks of 128
+    rows, 2 column tiles, GROUP_M 2, no XCD swizzle.  Group 2 (3 blocks) gets
+    2 bands (heights 2 and 1), column-major inside each."""
+    offs = [96, 352, 640, 1024]
+    got = O.fwd_tile_order(offs, 1024, 256, 128, 128, 2, 1)
+    ebc = [(0, 0, 0), (0, 0, 1),
+           (1, 0, 0), (1, 1, 0), (1, 0, 1), (1, 1, 1),
+           (2, 0, 0), (2, 1, 0), (2, 0, 1), (2, 1, 1), (2, 2, 0), (2, 2, 1),
+           (3, 0, 0), (3, 1, 0), (3, 0, 1), (3, 1, 1), (3, 2, 0), (3, 2, 1)]
+    start = {0: 0, 1: 96, 2: 352, 3: 640}
+    rows = {(0, 0): 96, (1, 0): 128, (1, 1): 128, (2, 0): 128, (2, 1): 128, (2, 2): 32,
+            (3, 0): 128, (3, 1): 128, (3, 2): 128}
+    want = [(e, start[e] + 128 * b, rows[(e, b)], 128 * c, 128) for e, b, c in ebc]
+    assert got.shape == ((8 + 3) * 2, 5)
+    assert [tuple(r) for r in got[:18].tolist()] == want
+    assert (got[18:] == -1).all()
+    # the XCD swizzle (D=18, X=8) permutes the same tiles
+    sw = O.fwd_tile_order(offs, 1024, 256, 128, 128, 2, 8)
+    assert [tuple(r) for r in sw[:3].tolist()] == [want[0], want[3], want[6]]
+    assert sorted(tuple(r) for r in sw[:18].tolist()) == sorted(want)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_fwd_tile_order_covers_each_output_once(seed):
+    """Brute force: every (row, column) of every group is computed by exactly
+    one program, and nothing at or past offs[-1]; empty groups, more than 64
+    groups, both tile sizes, several GROUP_M and XCD widths."""
+    rng = np.random.default_rng(seed)
+    E = int(rng.choice([1, 3, 8, 80]))
+    sizes = rng.integers(0, 5, size=E) * int(rng.choice([32, 96, 7]))
+    if E > 4:
+        sizes[rng.choice(E, E // 5, replace=False)] = 0
+    offs = np.cumsum(sizes).astype(np.int64)
+    M = int(offs[-1]) + int(rng.integers(0, 300))
+    N = int(rng.choice([96, 256, 700]))
+    for BM in (128, 256):
+        for gm in (1, 3, 12):
+            for xcd in (1, 8):
+                got = O.fwd_tile_order(offs, M, N, BM, BM, gm, xcd)
+                cover = np.zeros((M, N), np.int32)
+                for e, r0, rows, n0, cols in got.tolist():
+                    if e < 0:
+                        continue
+                    lo = offs[e - 1] if e else 0
+                    assert lo <= r0 and r0 + rows <= offs[e] and rows > 0 and 0 < cols <= BM
+                    cover[r0:r0 + rows, n0:n0 + cols] += 1
+                assert (cover[: int(offs[-1])] == 1).all() and (cover[int(offs[-1]):] == 0).all()
+
+
+def test_fwd_tile_order_reduces_to_reference_map():
+    """With one column tile, bands of one m-block and no swizzle, the build's
+    order is the reference's m-block order (kernels/forward.py:320-338)."""
+    for E, M, BM, seed in ((4, 1024, 128, 1), (8, 16640, 256, 2), (70, 4096, 128, 3)):
+        offs = O.generate_jagged_offs(E, M, 32, rng=random.Random(seed))
+        buf, gub = O.routing_table(offs, M, BM)
+        got = O.fwd_tile_order(offs, M, 64, BM, 64, 1, 1)
+        starts = [0] + [int(v) for v in offs[:-1]]
+        for pid, code in enumerate(buf[2 * E + 1:].tolist()):
+            if code < 0:
+                assert got[pid, 0] == -1
+            else:
+                e, b = code & 0xFFFF, code >> 16
+                assert (got[pid, 0], got[pid, 1]) == (e, starts[e] + b * BM)
+
+
 # ---------------------------------------------------------------- grouped GEMMs
 
 
