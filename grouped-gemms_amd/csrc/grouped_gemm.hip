@@ -32,6 +32,7 @@
 //     stages; each MFMA takes its lane's byte at op_sel 0.
 //   * one workgroup barrier per stage; fragment and scale registers alternate
 //     between two sets (loop body unrolled twice).
+#include <mutex>
 #include <type_traits>
 
 #include "mxgg_device.h"
@@ -1729,13 +1730,13 @@ extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, in
   return part ? align256(sc) + part : sc;
 }
 
-extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
-                               const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
-                               const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
-                               const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
-                               void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
-                               int group_m, int xcd, void* workspace, size_t ws_bytes, void* stream) {
-  clear_error();
+// Argument checks of a forward call shared by the entry points; MXGG_OK
+// when the call may go ahead (check *empty: nothing to compute).
+static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas, const uint8_t* B,
+                            int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
+                            int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                            const void* out, int out_dtype, int64_t ldo, bool* empty) {
+  *empty = false;
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: weight format %d not E4M3/E2M1", b_fmt);
   if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F16 && out_dtype != MXGG_DTYPE_F32)
@@ -1754,15 +1755,25 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
     return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: row strides must be below 2**23 bytes");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: dimension above 2**31");
-  if (M == 0 || N == 0) return MXGG_OK;
+  if (M == 0 || N == 0) {
+    *empty = true;
+    return MXGG_OK;
+  }
   if (!A || !A_s || !B || !B_s || !offs || !out)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: null pointer");
+  if (fwd_scale_bytes(E, M, N, K) >= ((size_t)1 << 31))
+    return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: problem too large");
+  return MXGG_OK;
+}
+
+// A checked forward call: re-lay the scales into the workspace, then the
+// GEMM launches (the partial-tile area after the scales, when there is room).
+static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas, const uint8_t* B,
+                          int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
+                          int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
+                          int out_dtype, int64_t ldo, int block_m, int block_n, int group_m, int xcd,
+                          void* workspace, size_t ws_bytes, void* stream) {
   const size_t need = fwd_scale_bytes(E, M, N, K);
-  if (need >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: problem too large");
-  if (need && (!workspace || ws_bytes < need))
-    return fail(MXGG_ERR_WORKSPACE, "grouped_mm: workspace of at least %zu bytes needed, %zu given", need,
-                workspace ? ws_bytes : (size_t)0);
-  if (int rc = require_device()) return rc;
   FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
   const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
                                            : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
@@ -1788,6 +1799,91 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   if (c.bm == 256)
     return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, part_bytes, st);
   return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, part_bytes, st);
+}
+
+extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
+                               const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
+                               const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
+                               const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                               void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
+                               int group_m, int xcd, void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  bool empty;
+  if (int rc = check_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
+                                out, out_dtype, ldo, &empty))
+    return rc;
+  if (empty) return MXGG_OK;
+  const size_t need = fwd_scale_bytes(E, M, N, K);
+  if (need && (!workspace || ws_bytes < need))
+    return fail(MXGG_ERR_WORKSPACE, "grouped_mm: workspace of at least %zu bytes needed, %zu given", need,
+                workspace ? ws_bytes : (size_t)0);
+  if (int rc = require_device()) return rc;
+  return run_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K, out,
+                        out_dtype, ldo, block_m, block_n, group_m, xcd, workspace, ws_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free forward entry point: the workspace is a device array of
+// this library (one per GPU) instead of caller memory
+// ---------------------------------------------------------------------------
+
+// MXGG_NOALLOC_SCRATCH_BYTES per device, held from the library's load to the
+// end of the process: the re-laid scales of a call (4 * cdiv(K, 128) *
+// (M + E*N) bytes; 21 MB for the largest sweep shape) and, after them, the
+// fp32 partial tiles of a split last round.  Nothing in it needs clearing:
+// every call writes the scales before reading them, and a split call writes
+// every partial tile before the reduce reads it.
+static __device__ __align__(256) uint8_t scratch[MXGG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];   // device address of `scratch` per device; null until looked up
+}  // namespace
+
+// This device's copy of `scratch` (the host-side name is not a device
+// address): looked up once per device, with that device current.
+static int scratch_for_device(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MXGG_ERR_NO_DEVICE, "grouped_mm_noalloc: no HIP device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm_noalloc: device %d above 63", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : MXGG_ERR_UNSUPPORTED, "grouped_mm_noalloc: hipGetSymbolAddress: %s",
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MXGG_OK;
+}
+
+extern "C" int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
+                                       const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
+                                       const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
+                                       const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                                       void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
+                                       int group_m, int xcd, void* stream) {
+  clear_error();
+  bool empty;
+  if (int rc = check_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
+                                out, out_dtype, ldo, &empty))
+    return rc;
+  if (empty) return MXGG_OK;
+  const size_t need = fwd_scale_bytes(E, M, N, K);
+  if (need > (size_t)MXGG_NOALLOC_SCRATCH_BYTES)
+    return fail(MXGG_ERR_WORKSPACE,
+                "grouped_mm_noalloc: the re-laid scales need %zu bytes, more than the %zu-byte scratch "
+                "(4 * cdiv(K, 128) * (M + E*N) must stay within it)",
+                need, (size_t)MXGG_NOALLOC_SCRATCH_BYTES);
+  if (int rc = require_device()) return rc;
+  void* ws = nullptr;
+  if (int rc = scratch_for_device(&ws)) return rc;
+  return run_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K, out,
+                        out_dtype, ldo, block_m, block_n, group_m, xcd, ws, (size_t)MXGG_NOALLOC_SCRATCH_BYTES,
+                        stream);
 }
 
 extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,

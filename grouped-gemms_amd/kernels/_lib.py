@@ -21,6 +21,7 @@ ERR_INVALID_ARG = -1
 ERR_UNSUPPORTED = -2
 ERR_WORKSPACE = -3
 ERR_NO_DEVICE = -4
+NOALLOC_SCRATCH_BYTES = 48 << 20   # MXGG_NOALLOC_SCRATCH_BYTES
 FMT_E4M3 = 0
 FMT_E2M1 = 4
 DTYPE_BF16 = 0
@@ -55,6 +56,12 @@ SIGNATURES = {
                                  _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
                                  _c_p, _c_i32, _c_i64,
                                  _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
+    "mxgg_grouped_mm_noalloc": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
+                                         _c_p, _c_i32, _c_i64, _c_i64,
+                                         _c_p, _c_i64, _c_i64,
+                                         _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
+                                         _c_p, _c_i32, _c_i64,
+                                         _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
     "mxgg_grouped_mm_config": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32,
                                         ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32),
                                         ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32)]),

@@ -185,6 +185,28 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
                     void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * mxgg_grouped_mm without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  Same arguments,
+ * results and errors as mxgg_grouped_mm given a workspace of
+ * MXGG_NOALLOC_SCRATCH_BYTES bytes; the workspace is instead a device array
+ * inside this library, one per GPU, allocated when the library is loaded and
+ * held until the process ends.  Calls it cannot take -- the re-laid scales,
+ * 4 * ceil(K/128) * (M + E*N) bytes, above MXGG_NOALLOC_SCRATCH_BYTES -- are
+ * rejected with MXGG_ERR_WORKSPACE before anything is launched.  The call
+ * itself allocates nothing.  Every call on a GPU uses that GPU's one array:
+ * calls that overlap on one GPU (other streams, other threads) race and give
+ * wrong results; serialise them.
+ */
+#define MXGG_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
+int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
+                            const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
+                            const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
+                            const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                            void* out, int out_dtype, int64_t ldo,
+                            int block_m, int block_n, int group_m, int xcd_swizzle, void* stream);
+
+/*
  * Weight-gradient grouped GEMM: out[g] = GO[:, s:e] @ IA[:, s:e]^T, shape (E, N, K),
  * a reduction over each group's token range; an empty group gives zeros.
  * Replaces `triton_mxfp8_wgrad` (kernels/backward.py:217-305), including its
