@@ -1732,10 +1732,12 @@ extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, in
 
 // Argument checks of a forward call shared by the entry points; MXGG_OK
 // when the call may go ahead (check *empty: nothing to compute).
+// plain: A_s / B_s are plain scales with these strides (else step-major,
+// strides unused).
 static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas, const uint8_t* B,
                             int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
                             int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
-                            const void* out, int out_dtype, int64_t ldo, bool* empty) {
+                            const void* out, int out_dtype, int64_t ldo, bool plain, bool* empty) {
   *empty = false;
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: weight format %d not E4M3/E2M1", b_fmt);
@@ -1745,9 +1747,9 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: negative shape");
   if (K % 32) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: K=%lld must be a multiple of 32", (long long)K);
   const int64_t kb = b_fmt == MXGG_FMT_E2M1 ? K / 2 : K;
-  if (lda < K || ldas < K / 32 || ldb_n < kb || ldbs_n < K / 32 || ldo < N)
+  if (lda < K || ldb_n < kb || ldo < N || (plain && (ldas < K / 32 || ldbs_n < K / 32)))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: a row stride is smaller than its row");
-  if (E > 1 && (ldb_e < N * ldb_n || ldbs_e < N * ldbs_n))
+  if (E > 1 && (ldb_e < N * ldb_n || (plain && ldbs_e < N * ldbs_n)))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: expert stride smaller than one expert");
   if (lda % 16 || ldb_n % 16 || !aligned16(A) || !aligned16(B))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: A/B rows must be 16-byte aligned");
@@ -1766,18 +1768,38 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
   return MXGG_OK;
 }
 
-// A checked forward call: re-lay the scales into the workspace, then the
-// GEMM launches (the partial-tile area after the scales, when there is room).
+// The GEMM launches of a checked forward call on step-major scales (as: A
+// [T][M], bs: B [E][T][N] dwords); part / part_bytes: room for the fp32
+// partial tiles of a split last round (none: no tile is split).
+static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, const uint8_t* B, int b_fmt,
+                             int64_t ldb_n, int64_t ldb_e, const uint8_t* bs, const int32_t* offs, int E, int64_t M,
+                             int64_t N, int64_t K, void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
+                             int group_m, int xcd, void* part_area, size_t part_bytes, hipStream_t st) {
+  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
+  const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
+                                           : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
+  if (!built) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built", c.bm, c.bn);
+  const int64_t T = cdiv(K, STEP);
+  float* part = c.split && part_area && part_bytes ? (float*)part_area : nullptr;
+  FwdParams p{A, lda, B, ldb_n, ldb_e, as, (uint32_t)(4 * T * M), bs, (uint32_t)(4 * T * N), offs, E, M, N, K,
+              (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0};
+  const size_t pb = part ? part_bytes : 0;
+  if (b_fmt == MXGG_FMT_E2M1)
+    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
+  if (c.bm == 256)
+    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
+  return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, pb, st);
+}
+
+// A checked forward call on plain scales: re-lay them step-major into the
+// workspace, then the GEMM launches (partial tiles after the scales, when
+// there is room).
 static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas, const uint8_t* B,
                           int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
                           int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
                           int out_dtype, int64_t ldo, int block_m, int block_n, int group_m, int xcd,
                           void* workspace, size_t ws_bytes, void* stream) {
   const size_t need = fwd_scale_bytes(E, M, N, K);
-  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
-  const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
-                                           : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
-  if (!built) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built", c.bm, c.bn);
   hipStream_t st = (hipStream_t)stream;
   const int64_t T = cdiv(K, STEP);
   uint32_t* wsd = (uint32_t*)workspace;
@@ -1787,18 +1809,11 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
                                  "grouped_mm"))
       return rc;
   }
-  // partial tiles of a split last round after the scales (optional)
   const size_t part_off = align256(need);
-  float* part = c.split && ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
-  const size_t part_bytes = part ? ws_bytes - part_off : 0;
-  FwdParams p{A, lda, B, ldb_n, ldb_e, (const uint8_t*)workspace, (uint32_t)(4 * T * M),
-              (const uint8_t*)(wsd + T * M), (uint32_t)(4 * T * N), offs, E, M, N, K,
-              (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0};
-  if (b_fmt == MXGG_FMT_E2M1)
-    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, part_bytes, st);
-  if (c.bm == 256)
-    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, part_bytes, st);
-  return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, part_bytes, st);
+  void* part = ws_bytes > part_off ? (void*)((uint8_t*)workspace + part_off) : nullptr;
+  return launch_grouped_mm(A, lda, (const uint8_t*)wsd, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)(wsd + T * M), offs,
+                           E, M, N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, part,
+                           part ? ws_bytes - part_off : 0, st);
 }
 
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
@@ -1810,7 +1825,7 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   clear_error();
   bool empty;
   if (int rc = check_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
-                                out, out_dtype, ldo, &empty))
+                                out, out_dtype, ldo, true, &empty))
     return rc;
   if (empty) return MXGG_OK;
   const size_t need = fwd_scale_bytes(E, M, N, K);
@@ -1820,6 +1835,25 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   if (int rc = require_device()) return rc;
   return run_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K, out,
                         out_dtype, ldo, block_m, block_n, group_m, xcd, workspace, ws_bytes, stream);
+}
+
+extern "C" int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32_t* A_ss, const uint8_t* B,
+                                     int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint32_t* B_ss,
+                                     const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
+                                     int out_dtype, int64_t ldo, int block_m, int block_n, int group_m, int xcd,
+                                     void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  bool empty;
+  if (int rc = check_grouped_mm(A, lda, (const uint8_t*)A_ss, 0, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)B_ss, 0, 0,
+                                offs, E, M, N, K, out, out_dtype, ldo, false, &empty))
+    return rc;
+  if (empty) return MXGG_OK;
+  if (((uintptr_t)A_ss | (uintptr_t)B_ss) & 3)
+    return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_steps: step-major scales must be 4-byte aligned");
+  if (int rc = require_device()) return rc;
+  return launch_grouped_mm(A, lda, (const uint8_t*)A_ss, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)B_ss, offs, E, M,
+                           N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, workspace,
+                           workspace ? ws_bytes : 0, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1869,7 +1903,7 @@ extern "C" int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint
   clear_error();
   bool empty;
   if (int rc = check_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
-                                out, out_dtype, ldo, &empty))
+                                out, out_dtype, ldo, true, &empty))
     return rc;
   if (empty) return MXGG_OK;
   const size_t need = fwd_scale_bytes(E, M, N, K);
@@ -1924,17 +1958,18 @@ extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t
   return part ? align256(sc) + part : sc;
 }
 
-extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
-                          const uint8_t* ia_t, int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias,
-                          const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
-                          int out_dtype, void* workspace, size_t ws_bytes, void* stream) {
-  clear_error();
+// Argument checks of a wgrad call (plain: go_s / ia_s are plain scales with
+// these strides); *empty: nothing to compute.
+static int check_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos, const uint8_t* ia_t,
+                       int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias, const int32_t* offs, int E, int64_t M,
+                       int64_t N, int64_t K, const void* out, int out_dtype, bool plain, bool* empty) {
+  *empty = false;
   if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: out_dtype %d not BF16/F32", out_dtype);
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "wgrad: E=%d out of range", E);
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "wgrad: negative shape");
   if (M % 32) return fail(MXGG_ERR_INVALID_ARG, "wgrad: M=%lld must be a multiple of 32", (long long)M);
-  if (ld_go < M || ld_ia < M || ld_gos < M / 32 || ld_ias < M / 32)
+  if (ld_go < M || ld_ia < M || (plain && (ld_gos < M / 32 || ld_ias < M / 32)))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: a row stride is smaller than its row");
   if (ld_go % 16 || ld_ia % 16 || !aligned16(go_t) || !aligned16(ia_t))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: operand rows must be 16-byte aligned");
@@ -1942,28 +1977,26 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
     return fail(MXGG_ERR_UNSUPPORTED, "wgrad: row strides must be below 2**23 bytes");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return fail(MXGG_ERR_UNSUPPORTED, "wgrad: dimension above 2**31");
-  if (N == 0 || K == 0) return MXGG_OK;
+  if (N == 0 || K == 0) {
+    *empty = true;
+    return MXGG_OK;
+  }
   if (!go_t || !go_s || !ia_t || !ia_s || !offs || !out)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: null pointer");
-  const size_t need = wgrad_scale_bytes(M, N, K);
-  if (need >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: problem too large");
-  if (need && (!workspace || ws_bytes < need))
-    return fail(MXGG_ERR_WORKSPACE, "wgrad: workspace of at least %zu bytes needed, %zu given", need,
-                workspace ? ws_bytes : (size_t)0);
-  if (int rc = require_device()) return rc;
+  if (wgrad_scale_bytes(M, N, K) >= ((size_t)1 << 31)) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: problem too large");
+  return MXGG_OK;
+}
+
+// The wgrad launches of a checked call on step-major scales (gs: GO [T][N],
+// is: IA [T][K] dwords); part / part_bytes: room for the fp32 partial tiles
+// of tiles cut along the tokens (none: no tile is cut).
+static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, const uint8_t* ia_t, int64_t ld_ia,
+                        const uint8_t* is, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
+                        int out_dtype, void* part_area, size_t part_bytes, hipStream_t st) {
   typedef CfgF8_256 C;
-  hipStream_t st = (hipStream_t)stream;
   const int64_t T = cdiv(M, STEP);
-  uint32_t* wsd = (uint32_t*)workspace;
-  if (T > 0) {
-    if (int rc = launch_relayout(scale_job(go_s, ld_gos, 0, wsd, N, 1, M / 32, T),
-                                 scale_job(ia_s, ld_ias, 0, wsd + T * N, K, 1, M / 32, T), st, "wgrad"))
-      return rc;
-  }
-  const size_t part_off = align256(need);
-  float* part = ws_bytes > part_off ? (float*)((uint8_t*)workspace + part_off) : nullptr;
-  WgradParams p{go_t, ld_go, ia_t, ld_ia, (const uint8_t*)workspace, (uint32_t)(4 * T * N),
-                (const uint8_t*)(wsd + T * N), (uint32_t)(4 * T * K), offs, E, M, N, K,
+  float* part = part_area && part_bytes ? (float*)part_area : nullptr;
+  WgradParams p{go_t, ld_go, ia_t, ld_ia, gs, (uint32_t)(4 * T * N), is, (uint32_t)(4 * T * K), offs, E, M, N, K,
                 (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0, 0, 0, 0};
   const int64_t tiles = (int64_t)E * p.tiles_n * p.tiles_k;
   if (tiles > INT32_MAX / 2) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");
@@ -1972,7 +2005,7 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   // groups differ in length, and with them the tiles' run times: with E > 1
   // only a lone under-filled round is split (its tiles all start at once)
   const bool may_split = E == 1 || tiles < par;
-  const int slots = part && may_split ? split_slots<C>(ws_bytes - part_off) : 0;
+  const int slots = part && may_split ? split_slots<C>(part_bytes) : 0;
   constexpr int kib = C::BM * C::BN * 4 / 1024;
   const Split sp = split_plan((int)tiles, par, (int)wgrad_group_steps(E, M), slots, kib);
   p.dp = sp.dp;
@@ -2005,4 +2038,50 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   hipLaunchKernelGGL((wgrad_reduce_kernel<C>), dim3((unsigned)(split_tiles_ub * ReduceShape<C>::CH)), dim3(256),
                      0, st, p);
   return launch_status("wgrad");
+}
+
+extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
+                          const uint8_t* ia_t, int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias,
+                          const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
+                          int out_dtype, void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  bool empty;
+  if (int rc = check_wgrad(go_t, ld_go, go_s, ld_gos, ia_t, ld_ia, ia_s, ld_ias, offs, E, M, N, K, out, out_dtype,
+                           true, &empty))
+    return rc;
+  if (empty) return MXGG_OK;
+  const size_t need = wgrad_scale_bytes(M, N, K);
+  if (need && (!workspace || ws_bytes < need))
+    return fail(MXGG_ERR_WORKSPACE, "wgrad: workspace of at least %zu bytes needed, %zu given", need,
+                workspace ? ws_bytes : (size_t)0);
+  if (int rc = require_device()) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t T = cdiv(M, STEP);
+  uint32_t* wsd = (uint32_t*)workspace;
+  if (T > 0) {
+    if (int rc = launch_relayout(scale_job(go_s, ld_gos, 0, wsd, N, 1, M / 32, T),
+                                 scale_job(ia_s, ld_ias, 0, wsd + T * N, K, 1, M / 32, T), st, "wgrad"))
+      return rc;
+  }
+  const size_t part_off = align256(need);
+  void* part = ws_bytes > part_off ? (void*)((uint8_t*)workspace + part_off) : nullptr;
+  return launch_wgrad(go_t, ld_go, (const uint8_t*)wsd, ia_t, ld_ia, (const uint8_t*)(wsd + T * N), offs, E, M, N, K,
+                      out, out_dtype, part, part ? ws_bytes - part_off : 0, st);
+}
+
+extern "C" int mxgg_wgrad_steps(const uint8_t* go_t, int64_t ld_go, const uint32_t* go_ss, const uint8_t* ia_t,
+                                int64_t ld_ia, const uint32_t* ia_ss, const int32_t* offs, int E, int64_t M,
+                                int64_t N, int64_t K, void* out, int out_dtype, void* workspace, size_t ws_bytes,
+                                void* stream) {
+  clear_error();
+  bool empty;
+  if (int rc = check_wgrad(go_t, ld_go, (const uint8_t*)go_ss, 0, ia_t, ld_ia, (const uint8_t*)ia_ss, 0, offs, E, M,
+                           N, K, out, out_dtype, false, &empty))
+    return rc;
+  if (empty) return MXGG_OK;
+  if (((uintptr_t)go_ss | (uintptr_t)ia_ss) & 3)
+    return fail(MXGG_ERR_INVALID_ARG, "wgrad_steps: step-major scales must be 4-byte aligned");
+  if (int rc = require_device()) return rc;
+  return launch_wgrad(go_t, ld_go, (const uint8_t*)go_ss, ia_t, ld_ia, (const uint8_t*)ia_ss, offs, E, M, N, K, out,
+                      out_dtype, workspace, workspace ? ws_bytes : 0, (hipStream_t)stream);
 }

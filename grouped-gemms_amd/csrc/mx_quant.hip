@@ -15,10 +15,38 @@
 // row-wise blocks, so one read of the source gives to_mx(x) and
 // to_mx(x.t().contiguous()): 2 + 2 * (1 + 1/32) = 4.06 bytes per bf16
 // element instead of 6.06 for the two passes.
+//
+// Scales go out in the reference's plain layout (row-major (rows, blocks)
+// bytes) or step-major, the layout the GEMM kernels read (MXGG_SCALES_STEPS:
+// for batches of R rows, dword (b, t, r) holds blocks 4t .. 4t+3 of row
+// b*R + r, bytes past the row's last block 127), so a GEMM given them skips
+// its per-call re-layout.
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
 namespace mxgg {
+
+// Destination of a quantizer's scale bytes.  Row r counts over every batch.
+struct ScaleOut {
+  uint8_t* p;
+  int64_t ld;       // plain: row stride; steps: R, rows per batch
+  int64_t T;        // steps: dwords per row (cdiv(blocks, 4))
+  int nblk;         // blocks per row
+  bool steps;
+};
+
+__device__ __forceinline__ void put_scale(const ScaleOut& o, int64_t r, int64_t blk, uint32_t s) {
+  if (!o.steps) {
+    o.p[r * o.ld + blk] = (uint8_t)s;
+    return;
+  }
+  const int64_t b = r / o.ld, rr = r - b * o.ld;
+  uint8_t* d = o.p + ((b * o.T + (blk >> 2)) * o.ld + rr) * 4;
+  const int j = (int)(blk & 3);
+  d[j] = (uint8_t)s;
+  if (blk == o.nblk - 1)                 // the last step's bytes past the row: neutral 2**0
+    for (int k = j + 1; k < 4; ++k) d[k] = 127;
+}
 
 template <int SRC>
 __device__ __forceinline__ void load8(const uint8_t* p, float (&v)[8]) {
@@ -56,8 +84,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restri
                                                          int64_t rows, int64_t cols,
                                                          int64_t ld_src_bytes,
                                                          uint8_t* __restrict__ q, int64_t ld_q,
-                                                         uint8_t* __restrict__ scales,
-                                                         int64_t ld_s) {
+                                                         ScaleOut so) {
   const int64_t bpr = cols / 32;                       // blocks per row
   const int64_t nblk = rows * bpr;
   const int sub = threadIdx.x & 3;                     // which 8 of the 32
@@ -95,7 +122,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restri
       for (int i = 0; i < 8; ++i) w |= e2m1_code(v[i], mul) << (4 * i);
       *reinterpret_cast<uint32_t*>(q + r * ld_q + col / 2) = w;
     }
-    if (sub == 0) scales[r * ld_s + cb] = (uint8_t)s;
+    if (sub == 0) put_scale(so, r, cb, s);
   }
 }
 
@@ -106,8 +133,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint8_t* __restri
                                                          int64_t rows, int64_t cols,
                                                          int64_t ld_src_bytes,
                                                          uint8_t* __restrict__ q, int64_t ld_q,
-                                                         uint8_t* __restrict__ scales,
-                                                         int64_t ld_s) {
+                                                         ScaleOut so) {
   constexpr int EB = elem_bytes<SRC>();
   constexpr int TC = 256;                         // tile columns
   __shared__ __attribute__((aligned(16))) uint8_t tile[32 * TC * EB];
@@ -159,7 +185,7 @@ __global__ __launch_bounds__(256) void quant_cols_kernel(const uint8_t* __restri
   uint8_t* dst = q + col * ld_q + r0;
   *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
   *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-  scales[col * ld_s + r0 / 32] = (uint8_t)s;
+  put_scale(so, col, r0 / 32, s);
 }
 
 // Row-wise and column-wise quantization of one 32 x 256 tile of batch
@@ -169,19 +195,15 @@ template <int SRC>
 __global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restrict__ src,
                                                          int64_t rows, int64_t cols,
                                                          int64_t ld_src_bytes,
-                                                         uint8_t* __restrict__ q_r, int64_t ld_qr,
-                                                         uint8_t* __restrict__ s_r, int64_t ld_sr,
-                                                         uint8_t* __restrict__ q_c, int64_t ld_qc,
-                                                         uint8_t* __restrict__ s_c, int64_t ld_sc) {
+                                                         uint8_t* __restrict__ q_r, int64_t ld_qr, ScaleOut s_r,
+                                                         uint8_t* __restrict__ q_c, int64_t ld_qc, ScaleOut s_c) {
   constexpr int EB = elem_bytes<SRC>();
   constexpr int TC = 256;
   __shared__ __attribute__((aligned(16))) uint8_t tile[32 * TC * EB];
   const int64_t b = blockIdx.z;
   src += b * rows * ld_src_bytes;
   q_r += b * rows * ld_qr;
-  s_r += b * rows * ld_sr;
   q_c += b * cols * ld_qc;
-  s_c += b * cols * ld_sc;
   const int64_t r0 = (int64_t)blockIdx.y * 32;
   const int64_t c0 = (int64_t)blockIdx.x * TC;
   const int t = threadIdx.x;
@@ -202,7 +224,8 @@ __global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restri
     else if constexpr (SRC == MXGG_DTYPE_F16) return (float)*reinterpret_cast<const _Float16*>(p);
     else return *reinterpret_cast<const float*>(p);
   };
-  auto quant32 = [&](const float (&v)[32], uint8_t* dst, uint8_t* sdst) {
+  // block blk of global row r (over every batch) of scale output so
+  auto quant32 = [&](const float (&v)[32], uint8_t* dst, const ScaleOut& so, int64_t r, int64_t blk) {
     uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
@@ -220,7 +243,7 @@ __global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restri
     }
     *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
     *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-    *sdst = (uint8_t)sc;
+    put_scale(so, r, blk, sc);
   };
   {
     const int rr = t / 8, cb = t % 8;
@@ -229,7 +252,7 @@ __global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restri
       float v[32];
 #pragma unroll
       for (int i = 0; i < 32; ++i) v[i] = load(rr, cb * 32 + i);
-      quant32(v, q_r + (r0 + rr) * ld_qr + col0, s_r + (r0 + rr) * ld_sr + col0 / 32);
+      quant32(v, q_r + (r0 + rr) * ld_qr + col0, s_r, b * rows + r0 + rr, col0 / 32);
     }
   }
   {
@@ -238,7 +261,7 @@ __global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restri
       float v[32];
 #pragma unroll
       for (int rr = 0; rr < 32; ++rr) v[rr] = load(rr, t);
-      quant32(v, q_c + col * ld_qc + r0, s_c + col * ld_sc + r0 / 32);
+      quant32(v, q_c + col * ld_qc + r0, s_c, b * cols + col, r0 / 32);
     }
   }
 }
@@ -247,9 +270,33 @@ __global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restri
 
 using namespace mxgg;
 
+namespace {
+
+// Scale destination for `out_rows` rows of `nblk` blocks; MXGG_OK or a
+// failure naming `what`.
+int scale_out(const char* what, uint8_t* p, int64_t ld_s, int layout, int64_t out_rows, int64_t nblk, ScaleOut* o) {
+  if (layout != MXGG_SCALES_PLAIN && layout != MXGG_SCALES_STEPS)
+    return fail(MXGG_ERR_INVALID_ARG, "%s: scale_layout %d not PLAIN/STEPS", what, layout);
+  o->p = p;
+  o->ld = ld_s;
+  o->T = (nblk + 3) / 4;
+  o->nblk = (int)nblk;
+  o->steps = layout == MXGG_SCALES_STEPS;
+  if (!o->steps) {
+    if (ld_s < nblk) return fail(MXGG_ERR_INVALID_ARG, "%s: scale row stride smaller than the row", what);
+  } else if (ld_s <= 0 || out_rows % ld_s) {
+    return fail(MXGG_ERR_INVALID_ARG, "%s: step-major scales need ld_s = rows per batch, dividing the %lld rows", what,
+                (long long)out_rows);
+  }
+  if (nblk > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "%s: rows too long", what);
+  return MXGG_OK;
+}
+
+}  // namespace
+
 extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
                                 int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
-                                uint8_t* scales, int64_t ld_s, void* stream) {
+                                uint8_t* scales, int64_t ld_s, int scale_layout, void* stream) {
   clear_error();
   if (src_dtype != MXGG_DTYPE_BF16 && src_dtype != MXGG_DTYPE_F16 && src_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: src_dtype %d not one of BF16/F16/F32", src_dtype);
@@ -259,8 +306,10 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
   if (cols % 32) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: last dim %lld must be divisible by block_size 32", (long long)cols);
   const int eb = src_dtype == MXGG_DTYPE_F32 ? 4 : 2;
   const int64_t qcols = elem_fmt == MXGG_FMT_E4M3 ? cols : cols / 2;
-  if (ld_src < cols || ld_q < qcols || ld_s < cols / 32)
+  if (ld_src < cols || ld_q < qcols)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: row stride smaller than the row");
+  ScaleOut so;
+  if (int rc = scale_out("quantize_mx", scales, ld_s, scale_layout, rows, cols / 32, &so)) return rc;
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q || !scales) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: null pointer");
   if (((uintptr_t)src % 16) || ((ld_src * eb) % 16))
@@ -276,7 +325,7 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
   uint8_t* q8 = (uint8_t*)q;
   const int64_t lsb = ld_src * eb;
 #define MXGG_QROWS(SRC, FMT) \
-  hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT>), dim3(grid), dim3(256), 0, st, s8, rows, cols, lsb, q8, ld_q, scales, ld_s)
+  hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT>), dim3(grid), dim3(256), 0, st, s8, rows, cols, lsb, q8, ld_q, so)
   if (elem_fmt == MXGG_FMT_E4M3) {
     if (src_dtype == MXGG_DTYPE_BF16) MXGG_QROWS(MXGG_DTYPE_BF16, MXGG_FMT_E4M3);
     else if (src_dtype == MXGG_DTYPE_F16) MXGG_QROWS(MXGG_DTYPE_F16, MXGG_FMT_E4M3);
@@ -292,7 +341,7 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
 
 extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t cols,
                                      int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
-                                     uint8_t* scales, int64_t ld_s, void* stream) {
+                                     uint8_t* scales, int64_t ld_s, int scale_layout, void* stream) {
   clear_error();
   if (src_dtype != MXGG_DTYPE_BF16 && src_dtype != MXGG_DTYPE_F16 && src_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: src_dtype %d not one of BF16/F16/F32", src_dtype);
@@ -301,8 +350,10 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
   if (rows < 0 || cols < 0) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: negative shape");
   if (rows % 32) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: dim 0 (%lld) must be divisible by block_size 32", (long long)rows);
   const int eb = src_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-  if (ld_src < cols || ld_q < rows || ld_s < rows / 32)
+  if (ld_src < cols || ld_q < rows)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: row stride smaller than the row");
+  ScaleOut so;
+  if (int rc = scale_out("quantize_mx_dim0", scales, ld_s, scale_layout, cols, rows / 32, &so)) return rc;
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q || !scales) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: null pointer");
   if (((uintptr_t)src % 16) || ((ld_src * eb) % 16) || ((cols * eb) % 16))
@@ -316,18 +367,18 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
   const uint8_t* s8 = (const uint8_t*)src;
   const int64_t lsb = ld_src * eb;
   if (src_dtype == MXGG_DTYPE_BF16)
-    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_BF16>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, scales, ld_s);
+    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_BF16>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, so);
   else if (src_dtype == MXGG_DTYPE_F16)
-    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F16>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, scales, ld_s);
+    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F16>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, so);
   else
-    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F32>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, scales, ld_s);
+    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F32>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, so);
   return launch_status("quantize_mx_dim0");
 }
 
 extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
                                      int64_t ld_src, void* q_rows, int64_t ld_qr, uint8_t* s_rows,
                                      int64_t ld_sr, void* q_cols, int64_t ld_qc, uint8_t* s_cols,
-                                     int64_t ld_sc, void* stream) {
+                                     int64_t ld_sc, int scale_layout, void* stream) {
   clear_error();
   if (src_dtype != MXGG_DTYPE_BF16 && src_dtype != MXGG_DTYPE_F16 && src_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: src_dtype %d not one of BF16/F16/F32", src_dtype);
@@ -335,8 +386,11 @@ extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t bat
   if (rows % 32 || cols % 32)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: both dims (%lld, %lld) must be divisible by block_size 32",
                 (long long)rows, (long long)cols);
-  if (ld_src < cols || ld_qr < cols || ld_sr < cols / 32 || ld_qc < rows || ld_sc < rows / 32)
+  if (ld_src < cols || ld_qr < cols || ld_qc < rows)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: row stride smaller than the row");
+  ScaleOut sr, sc;
+  if (int rc = scale_out("quantize_mx_both", s_rows, ld_sr, scale_layout, batch * rows, cols / 32, &sr)) return rc;
+  if (int rc = scale_out("quantize_mx_both", s_cols, ld_sc, scale_layout, batch * cols, rows / 32, &sc)) return rc;
   if (batch == 0 || rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q_rows || !s_rows || !q_cols || !s_cols)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: null pointer");
@@ -353,7 +407,7 @@ extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t bat
   const int64_t lsb = ld_src * eb;
 #define MXGG_QBOTH(SRC)                                                                                  \
   hipLaunchKernelGGL(quant_both_kernel<SRC>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q_rows, \
-                     ld_qr, s_rows, ld_sr, (uint8_t*)q_cols, ld_qc, s_cols, ld_sc)
+                     ld_qr, sr, (uint8_t*)q_cols, ld_qc, sc)
   if (src_dtype == MXGG_DTYPE_BF16) MXGG_QBOTH(MXGG_DTYPE_BF16);
   else if (src_dtype == MXGG_DTYPE_F16) MXGG_QBOTH(MXGG_DTYPE_F16);
   else MXGG_QBOTH(MXGG_DTYPE_F32);

@@ -13,11 +13,8 @@ import torch
 from . import _lib
 
 
-def _is_rocm() -> bool:
-    return getattr(torch.version, "hip", None) is not None
-
-
-_rocm_mxfp8_available = _is_rocm() and _lib.available()
+# A ROCm build of torch (torch.version.hip set) with libmxgg loadable.
+_rocm_mxfp8_available = bool(getattr(torch.version, "hip", None)) and _lib.available()
 
 _UNAVAILABLE_MSG = "ROCm MXFP8 kernels require gfx950 and the libmxgg extension"
 

@@ -27,6 +27,8 @@ FMT_E2M1 = 4
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 DTYPE_F32 = 2
+SCALES_PLAIN = 0
+SCALES_STEPS = 1
 
 _c_i32 = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -39,11 +41,11 @@ SIGNATURES = {
     "mxgg_last_error_string": (ctypes.c_char_p, []),
     "mxgg_device_supported": (_c_i32, []),
     "mxgg_quantize_mx": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64,
-                                  _c_p, _c_i64, _c_p]),
+                                  _c_p, _c_i64, _c_i32, _c_p]),
     "mxgg_quantize_mx_dim0": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_i64,
-                                       _c_p, _c_i64, _c_p]),
+                                       _c_p, _c_i64, _c_i32, _c_p]),
     "mxgg_quantize_mx_both": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,
-                                       _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
+                                       _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_p]),
     "mxgg_routing_words": (_c_i64, [_c_i32, _c_i64, _c_i32]),
     "mxgg_build_routing": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i32, _c_p, _c_p]),
     "mxgg_schedule_programs": (_c_i64, [_c_i32, _c_i64, _c_i64, _c_i32, _c_i32]),
@@ -56,6 +58,11 @@ SIGNATURES = {
                                  _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
                                  _c_p, _c_i32, _c_i64,
                                  _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
+    "mxgg_grouped_mm_steps": (_c_i32, [_c_p, _c_i64, _c_p,
+                                       _c_p, _c_i32, _c_i64, _c_i64, _c_p,
+                                       _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
+                                       _c_p, _c_i32, _c_i64,
+                                       _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
     "mxgg_grouped_mm_noalloc": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
                                          _c_p, _c_i32, _c_i64, _c_i64,
                                          _c_p, _c_i64, _c_i64,
@@ -70,6 +77,9 @@ SIGNATURES = {
                             _c_p, _c_i64, _c_p, _c_i64,
                             _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
                             _c_p, _c_i32, _c_p, _c_sz, _c_p]),
+    "mxgg_wgrad_steps": (_c_i32, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p,
+                                  _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
+                                  _c_p, _c_i32, _c_p, _c_sz, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -6,6 +6,9 @@ dim-1 quantized operands ``go_t (N, M)`` and ``ia_t (K, M)`` (scales per 32
 tokens), one reduction over each group's token range, output ``(E, N, K)``.
 As in the reference the stored values are rounded to bf16 whatever
 ``out_dtype`` is (backward.py:103, 214) and an empty group yields zeros.
+Step-major int32 scales (``(T, N)`` and ``(T, K)``, ``T = cdiv(M, 128)``, as
+``to_mx_dim0(..., scale_layout="steps")`` writes them) skip the per-call
+re-layout (``mxgg_wgrad_steps``).
 """
 
 from __future__ import annotations
@@ -14,6 +17,7 @@ import torch
 
 from . import _lib
 from ._common import _offsets, _out_code, _require, _rowmajor, _stream_handle, _u8
+from .forward import _split_room
 
 
 def triton_mxfp8_wgrad(
@@ -54,21 +58,37 @@ def triton_mxfp8_wgrad(
             raise TypeError(f"{name} dtype {t.dtype} is not float8_e4m3fn")
     if M % 32:
         raise ValueError(f"M={M} must be a multiple of the MX block size 32")
-    if tuple(go_scale.shape) != (N, M // 32):
-        raise ValueError(f"go_scale shape {tuple(go_scale.shape)} != {(N, M // 32)}")
-    if tuple(ia_scale.shape) != (K, M // 32):
-        raise ValueError(f"ia_scale shape {tuple(ia_scale.shape)} != {(K, M // 32)}")
+    steps = go_scale.dtype == torch.int32
+    if steps != (ia_scale.dtype == torch.int32):
+        raise TypeError("go_scale and ia_scale must both be e8m0 bytes or both step-major int32")
+    T = (M + 127) // 128
+    want_g, want_i = ((T, N), (T, K)) if steps else ((N, M // 32), (K, M // 32))
+    if tuple(go_scale.shape) != want_g:
+        raise ValueError(f"go_scale shape {tuple(go_scale.shape)} != {want_g}")
+    if tuple(ia_scale.shape) != want_i:
+        raise ValueError(f"ia_scale shape {tuple(ia_scale.shape)} != {want_i}")
     E = group_end_offsets.shape[0]
     dev = go_t.device
     g = _u8(_rowmajor(go_t))
     a = _u8(_rowmajor(ia_t))
-    gs = _u8(_rowmajor(go_scale))
-    as_ = _u8(_rowmajor(ia_scale))
     offs = _offsets(group_end_offsets, dev)
     code = _out_code(out_dtype, allowed=(torch.bfloat16, torch.float32))
     out = torch.empty((E, N, K), dtype=out_dtype, device=dev)
     lib = _lib.load()
     ws_bytes = lib.mxgg_wgrad_workspace_size(E, M, N, K)
+    if steps:
+        gss, iss = go_scale.contiguous(), ia_scale.contiguous()
+        ws_bytes = _split_room(ws_bytes, 4 * T * (N + K))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        rc = lib.mxgg_wgrad_steps(
+            g.data_ptr(), g.stride(0), gss.data_ptr(), a.data_ptr(), a.stride(0), iss.data_ptr(),
+            offs.data_ptr(), E, M, N, K,
+            out.data_ptr(), code, ws.data_ptr() if ws is not None else None, ws_bytes,
+            _stream_handle(dev))
+        _lib.check(rc)
+        return out
+    gs = _u8(_rowmajor(go_scale))
+    as_ = _u8(_rowmajor(ia_scale))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_wgrad(
         g.data_ptr(), g.stride(0), gs.data_ptr(), gs.stride(0),

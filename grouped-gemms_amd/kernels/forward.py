@@ -11,7 +11,10 @@ piece and reduce launches.
 
 Beyond the reference, the weight may be MXFP4: ``weight`` of dtype
 ``torch.float4_e2m1fn_x2`` (or uint8) with last dim K/2, two e2m1 values per
-byte (element 2i in the low nibble), scales per 32 elements of K.
+byte (element 2i in the low nibble), scales per 32 elements of K.  And the
+scales may come step-major (int32 ``(T, M)`` and ``(E, T, N)``,
+``T = cdiv(K, 128)``, as ``to_mx(..., scale_layout="steps")`` writes them):
+the call then skips the re-layout launch (``mxgg_grouped_mm_steps``).
 """
 
 from __future__ import annotations
@@ -25,6 +28,13 @@ from ._common import _offsets, _out_code, _require, _rowmajor, _stream_handle, _
 BUILT_TILES = ((256, 256), (128, 128))
 
 _FP4_DTYPES = tuple(d for d in (getattr(torch, "float4_e2m1fn_x2", None), torch.uint8) if d is not None)
+
+
+def _split_room(total: int, scale_bytes: int) -> int:
+    """Partial-tile room of a workspace of ``total`` bytes whose first
+    ``scale_bytes`` (256-byte aligned) hold re-laid scales: what a call on
+    step-major scales gets, so that both calls make the same split plan."""
+    return max(0, total - ((scale_bytes + 255) // 256) * 256)
 
 
 def _pick_config(E: int, M: int, N: int, K: int, b_fmt: int = _lib.FMT_E4M3, BLOCK_M: int = 0,
@@ -99,10 +109,15 @@ def triton_mxfp8_grouped_mm(
         raise TypeError(f"input_act dtype {input_act.dtype} is not float8_e4m3fn")
     if K % 32:
         raise ValueError(f"K={K} must be a multiple of the MX block size 32")
-    if tuple(input_act_scales.shape) != (M, K // 32):
-        raise ValueError(f"input_act_scales shape {tuple(input_act_scales.shape)} != {(M, K // 32)}")
-    if tuple(weight_scales.shape) != (E, N, K // 32):
-        raise ValueError(f"weight_scales shape {tuple(weight_scales.shape)} != {(E, N, K // 32)}")
+    steps = input_act_scales.dtype == torch.int32
+    if steps != (weight_scales.dtype == torch.int32):
+        raise TypeError("input_act_scales and weight_scales must both be e8m0 bytes or both step-major int32")
+    T = (K + 127) // 128
+    want_a, want_b = ((T, M), (E, T, N)) if steps else ((M, K // 32), (E, N, K // 32))
+    if tuple(input_act_scales.shape) != want_a:
+        raise ValueError(f"input_act_scales shape {tuple(input_act_scales.shape)} != {want_a}")
+    if tuple(weight_scales.shape) != want_b:
+        raise ValueError(f"weight_scales shape {tuple(weight_scales.shape)} != {want_b}")
     if group_end_offsets.numel() != E:
         raise ValueError(f"group_end_offsets has {group_end_offsets.numel()} entries, weight has E={E}")
     # Tile requests are hints: a built tile is used, anything else (e.g. a
@@ -115,8 +130,6 @@ def triton_mxfp8_grouped_mm(
     dev = input_act.device
     a = _u8(_rowmajor(input_act))
     b = _u8(_rowmajor(weight))
-    a_s = _u8(_rowmajor(input_act_scales))
-    b_s = _u8(_rowmajor(weight_scales))
     offs = _offsets(group_end_offsets, dev)
     out = torch.empty((M, N), dtype=out_dtype, device=dev)
     code = _out_code(out_dtype)
@@ -125,6 +138,22 @@ def triton_mxfp8_grouped_mm(
     # split last round (overwritten by the call; torch's caching allocator
     # makes the per-call allocation cheap)
     ws_bytes = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
+    if steps:
+        a_ss, b_ss = input_act_scales.contiguous(), weight_scales.contiguous()
+        ws_bytes = _split_room(ws_bytes, 4 * T * (M + E * N))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        rc = lib.mxgg_grouped_mm_steps(
+            a.data_ptr(), a.stride(0), a_ss.data_ptr(),
+            b.data_ptr(), b_fmt, b.stride(1), b.stride(0), b_ss.data_ptr(),
+            offs.data_ptr(), E, M, N, K,
+            out.data_ptr(), code, out.stride(0),
+            int(bm), int(bn), int(GROUP_M or 0), int(XCD_SWIZZLE or 0),
+            ws.data_ptr() if ws is not None else None, ws_bytes,
+            _stream_handle(dev))
+        _lib.check(rc)
+        return out
+    a_s = _u8(_rowmajor(input_act_scales))
+    b_s = _u8(_rowmajor(weight_scales))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_grouped_mm(
         a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),

@@ -15,15 +15,18 @@ The reference ships the three GEMMs of an MoE layer's expert projection
             (the "dim1-quantized" operands, kernels/backward.py:232-243)
 
 Every operand is quantized by ``to_mx_both``, which reads the bf16 tensor once
-and writes both the row-wise and the transposed column-wise MX layouts.  The
-forward keeps only the e4m3 layouts the backward needs (x^T along M and w^T
-along N, with their scales): half the bytes of keeping x and w in bf16.
+and writes both the row-wise and the transposed column-wise MX layouts, with
+the scales step-major (``scale_layout="steps"``): the layout the GEMM kernels
+read, so none of the three GEMMs re-lays scales per call.  The forward keeps
+only the e4m3 layouts the backward needs (x^T along M and w^T along N, with
+their scales): half the bytes of keeping x and w in bf16.
 
-Groups are cumulative end offsets, multiples of 32 (the wgrad's 32-token
-scale blocks must not straddle groups), and every token must be routed:
-``offs[-1] == M``.  Rows past ``offs[-1]`` would get no output and no
-gradient (the GEMMs leave them unwritten, as the reference does), so the
-layer assumes there are none rather than synchronising to check.
+Groups are cumulative end offsets (any values; with bounds off the 32 grid a
+32-token scale block of the wgrad operands spans two groups and scales both,
+as in the reference), and every token must be routed: ``offs[-1] == M``.
+Rows past ``offs[-1]`` would get no output and no gradient (the GEMMs leave
+them unwritten, as the reference does), so the layer assumes there are none
+rather than synchronising to check.
 """
 
 from __future__ import annotations
@@ -40,8 +43,8 @@ from .quant import to_mx_both
 class _MXFP8GroupedMM(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, offs, out_dtype):
-        (sx, qx), (sxt, qxt) = to_mx_both(x)          # (M, K) along K; (K, M) along M
-        (sw, qw), (swt, qwt) = to_mx_both(w)          # (E, N, K) along K; (E, K, N) along N
+        (sx, qx), (sxt, qxt) = to_mx_both(x, scale_layout="steps")   # (M, K) along K; (K, M) along M
+        (sw, qw), (swt, qwt) = to_mx_both(w, scale_layout="steps")   # (E, N, K) along K; (E, K, N) along N
         out = triton_mxfp8_grouped_mm(qx, qw, sx, sw, offs, out_dtype=out_dtype)
         ctx.save_for_backward(qxt, sxt, qwt, swt, offs)
         ctx.x_dtype = x.dtype
@@ -51,7 +54,7 @@ class _MXFP8GroupedMM(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         qxt, sxt, qwt, swt, offs = ctx.saved_tensors
-        (sg, qg), (sgt, qgt) = to_mx_both(grad_out.contiguous())   # (M, N) along N; (N, M) along M
+        (sg, qg), (sgt, qgt) = to_mx_both(grad_out.contiguous(), scale_layout="steps")   # along N; (N, M) along M
         grad_x = grad_w = None
         if ctx.needs_input_grad[0]:
             grad_x = triton_mxfp8_grouped_mm(qg, qwt, sg, swt, offs, out_dtype=ctx.x_dtype)
@@ -68,7 +71,7 @@ def mxfp8_grouped_mm(x: torch.Tensor, w: torch.Tensor, offs: torch.Tensor,
     in ``x`` and ``w``.
 
     x: ``(M, K)`` bf16/fp16/fp32; w: ``(E, N, K)`` of the same kind; offs: ``(E,)``
-    int32 cumulative group ends on the device, multiples of 32, ``offs[-1] == M``.
+    int32 cumulative group ends on the device, ``offs[-1] == M``.
     M, N and K must be multiples of 32.  Returns ``(M, N)`` of ``out_dtype``.
     """
     if x.dim() != 2 or w.dim() != 3 or x.shape[1] != w.shape[2]:

@@ -8,6 +8,15 @@ instead of ~10 eager torch kernels.  ``to_mx_dim0`` produces
 "dim1-quantized" layout the weight gradient takes (kernels/backward.py:232).
 ``to_mx_both`` gives both layouts from one read of the source
 (``mxgg_quantize_mx_both``), for the backward pass of an MoE layer.
+
+``scale_layout="steps"`` makes any of them write the scales in the layout the
+GEMM kernels read (not the reference's: its CDNA4 pre-shuffle,
+kernels/forward.py:367-397, is redone on every call): an int32 tensor
+``(*batch, T, R)`` for a ``(*batch, R, L)`` result quantized along L,
+``T = cdiv(L, 128)``, element ``[t, r]`` holding the scale bytes of elements
+``128t .. 128t+127`` of row r (byte j: block 4t+j; bytes past the row 127).
+``triton_mxfp8_grouped_mm`` / ``triton_mxfp8_wgrad`` recognise such int32
+scales and skip their per-call re-layout.
 """
 
 from __future__ import annotations
@@ -28,13 +37,30 @@ def _src_code(t: torch.Tensor) -> int:
     return _SRC_CODES[t.dtype]
 
 
-def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32):
+def _layout_code(scale_layout: str) -> int:
+    if scale_layout == "plain":
+        return _lib.SCALES_PLAIN
+    if scale_layout == "steps":
+        return _lib.SCALES_STEPS
+    raise ValueError(f"scale_layout must be 'plain' or 'steps', got {scale_layout!r}")
+
+
+def step_scales_shape(batch: tuple, rows: int, length: int) -> tuple:
+    """Shape of step-major scales of ``(*batch, rows, length)`` quantized
+    along ``length``: ``(*batch, cdiv(length, 128), rows)`` (int32)."""
+    return tuple(batch) + ((length + 127) // 128, rows)
+
+
+def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32, *,
+          scale_layout: str = "plain"):
     """Quantize ``data`` along its last dim; returns ``(scales_u8, data_q)``.
 
     ``elem_dtype`` float8_e4m3fn gives ``data_q`` of ``data``'s shape;
     ``torch.float4_e2m1fn_x2`` gives packed fp4 with the last dim halved
     (element 2i in the low nibble).  ``scales_u8`` has the last dim divided
-    by 32.  Asserts like the reference (utils.py:78-81).
+    by 32.  Asserts like the reference (utils.py:78-81).  With
+    ``scale_layout="steps"`` the scales are step-major int32
+    ``(*data.shape[:-2], cdiv(L, 128), data.shape[-2])`` instead.
     """
     fp4 = _FP4 is not None and elem_dtype is _FP4
     assert elem_dtype is torch.float8_e4m3fn or fp4, "only e4m3fn and e2m1fn_x2 supported"
@@ -51,22 +77,34 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
         x = x.contiguous()
     rows = x.shape[0]
     qcols = L // 2 if fp4 else L
+    lay = _layout_code(scale_layout)
     q = torch.empty((rows, qcols), dtype=torch.uint8, device=data.device)
-    s = torch.empty((rows, L // 32), dtype=torch.uint8, device=data.device)
+    if lay == _lib.SCALES_STEPS:
+        R = shape[-2] if len(shape) >= 2 else 1
+        s = torch.empty(step_scales_shape(shape[:-2], R, L), dtype=torch.int32, device=data.device)
+        ld_s = R
+    else:
+        s = torch.empty((rows, L // 32), dtype=torch.uint8, device=data.device)
+        ld_s = L // 32
     lib = _lib.load()
     rc = lib.mxgg_quantize_mx(x.data_ptr(), code, rows, L, x.stride(0) if rows > 1 else L,
                               _lib.FMT_E2M1 if fp4 else _lib.FMT_E4M3,
-                              q.data_ptr(), qcols, s.data_ptr(), L // 32,
+                              q.data_ptr(), qcols, s.data_ptr(), ld_s, lay,
                               _stream_handle(data.device))
     _lib.check(rc)
     q = q.view(_FP4 if fp4 else torch.float8_e4m3fn).reshape(shape[:-1] + (qcols,))
+    if lay == _lib.SCALES_STEPS:
+        return s, q
     return s.reshape(shape[:-1] + (L // 32,)), q
 
 
-def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32):
+def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32, *,
+               scale_layout: str = "plain"):
     """``to_mx(data.t().contiguous())`` for a 2-D ``(R, C)`` tensor in one pass.
 
-    Returns ``(scales (C, R//32) uint8, data (C, R) float8_e4m3fn)``.
+    Returns ``(scales (C, R//32) uint8, data (C, R) float8_e4m3fn)``; with
+    ``scale_layout="steps"`` the scales are step-major int32
+    ``(cdiv(R, 128), C)``.
     """
     assert elem_dtype is torch.float8_e4m3fn, "to_mx_dim0 supports e4m3fn only"
     assert block_size == 32, "block_size must be 32 (OCP MX)"
@@ -81,23 +119,31 @@ def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
         x = x.contiguous()
     if (C * x.element_size()) % 16:
         raise ValueError(f"to_mx_dim0 needs dim 1 ({C}) to span a multiple of 16 bytes")
+    lay = _layout_code(scale_layout)
     q = torch.empty((C, R), dtype=torch.uint8, device=data.device)
-    s = torch.empty((C, R // 32), dtype=torch.uint8, device=data.device)
+    if lay == _lib.SCALES_STEPS:
+        s = torch.empty(step_scales_shape((), C, R), dtype=torch.int32, device=data.device)
+        ld_s = C
+    else:
+        s = torch.empty((C, R // 32), dtype=torch.uint8, device=data.device)
+        ld_s = R // 32
     lib = _lib.load()
     rc = lib.mxgg_quantize_mx_dim0(x.data_ptr(), code, R, C, x.stride(0), _lib.FMT_E4M3,
-                                   q.data_ptr(), R, s.data_ptr(), R // 32,
+                                   q.data_ptr(), R, s.data_ptr(), ld_s, lay,
                                    _stream_handle(data.device))
     _lib.check(rc)
     return s, q.view(torch.float8_e4m3fn)
 
 
-def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32):
+def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32, *,
+               scale_layout: str = "plain"):
     """``(to_mx(data), to_mx(data.transpose(-2, -1).contiguous()))`` in one pass.
 
     ``data`` is ``(R, C)`` or ``(B, R, C)`` with ``R`` and ``C`` multiples of
     32.  Returns ``((scales (.., R, C//32), data (.., R, C)),
     (scales (.., C, R//32), data (.., C, R)))``, e4m3, bit-identical to the
-    two separate calls.
+    two separate calls.  ``scale_layout="steps"``: step-major int32 scales
+    ``(.., cdiv(C, 128), R)`` and ``(.., cdiv(R, 128), C)``.
     """
     assert elem_dtype is torch.float8_e4m3fn, "to_mx_both supports e4m3fn only"
     assert block_size == 32, "block_size must be 32 (OCP MX)"
@@ -112,13 +158,20 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
     if (C * x.element_size()) % 16:
         raise ValueError(f"to_mx_both needs the last dim ({C}) to span a multiple of 16 bytes")
     dev = data.device
+    lay = _layout_code(scale_layout)
     q_r = torch.empty((B, R, C), dtype=torch.uint8, device=dev)
-    s_r = torch.empty((B, R, C // 32), dtype=torch.uint8, device=dev)
     q_c = torch.empty((B, C, R), dtype=torch.uint8, device=dev)
-    s_c = torch.empty((B, C, R // 32), dtype=torch.uint8, device=dev)
+    if lay == _lib.SCALES_STEPS:
+        s_r = torch.empty(step_scales_shape((B,), R, C), dtype=torch.int32, device=dev)
+        s_c = torch.empty(step_scales_shape((B,), C, R), dtype=torch.int32, device=dev)
+        ld_r, ld_c = R, C
+    else:
+        s_r = torch.empty((B, R, C // 32), dtype=torch.uint8, device=dev)
+        s_c = torch.empty((B, C, R // 32), dtype=torch.uint8, device=dev)
+        ld_r, ld_c = C // 32, R // 32
     lib = _lib.load()
-    rc = lib.mxgg_quantize_mx_both(x.data_ptr(), code, B, R, C, C, q_r.data_ptr(), C, s_r.data_ptr(), C // 32,
-                                   q_c.data_ptr(), R, s_c.data_ptr(), R // 32, _stream_handle(dev))
+    rc = lib.mxgg_quantize_mx_both(x.data_ptr(), code, B, R, C, C, q_r.data_ptr(), C, s_r.data_ptr(), ld_r,
+                                   q_c.data_ptr(), R, s_c.data_ptr(), ld_c, lay, _stream_handle(dev))
     _lib.check(rc)
     q_r, q_c = q_r.view(torch.float8_e4m3fn), q_c.view(torch.float8_e4m3fn)
     if data.dim() == 2:

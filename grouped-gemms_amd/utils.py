@@ -85,10 +85,10 @@ def generate_jagged_offs(E: int, M: int, multiple_of: int = 32, dtype=torch.int3
 
 
 def is_MI350() -> bool:
-    if getattr(torch.version, "hip", None) is None:
+    """Whether the current GPU is a gfx950 part (MI350X / MI355X) under a ROCm
+    build of torch (the reference asks the same of device 0, utils.py:108-115).
+    Never raises: no GPU, a CUDA or CPU build of torch all answer False."""
+    if not getattr(torch.version, "hip", None) or not torch.cuda.is_available():
         return False
-    try:
-        arch = torch.cuda.get_device_properties(0).gcnArchName
-    except Exception:
-        return False
-    return "gfx950" in arch
+    props = torch.cuda.get_device_properties(torch.cuda.current_device())
+    return props.gcnArchName.split(":")[0] == "gfx950"

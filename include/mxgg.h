@@ -21,6 +21,15 @@
  *          (rows, cols/32) with a row stride.
  * Strides are in ELEMENTS of the pointed-to tensor (bytes for e4m3 and scale
  * tensors, bytes -- i.e. element pairs -- for packed e2m1 tensors).
+ *
+ * Step-major scales (MXGG_SCALES_STEPS), the layout the GEMM kernels read:
+ * for an operand of `batch` matrices of R rows whose rows hold nblk scale
+ * bytes, T = ceil(nblk / 4) and dword (b, t, r) -- uint32 index
+ * (b*T + t)*R + r -- holds blocks 4t .. 4t+3 of row r of matrix b, block
+ * 4t+j in byte j; bytes past nblk are 127 (2**0).  The quantizers write it on
+ * request, and the *_steps GEMM entry points take it, skipping the per-call
+ * re-layout of plain scales.  (Not the reference's CDNA4 pre-shuffle,
+ * kernels/forward.py:367-397: one 128-element step of a row is one dword.)
  */
 #ifndef MXGG_H_
 #define MXGG_H_
@@ -50,6 +59,10 @@ extern "C" {
 #define MXGG_DTYPE_F16 1
 #define MXGG_DTYPE_F32 2
 
+/* scale layouts of the quantizer outputs */
+#define MXGG_SCALES_PLAIN 0   /* (rows, nblk) bytes, row stride ld_s */
+#define MXGG_SCALES_STEPS 1   /* step-major dwords (see above); ld_s = R, the rows per batch */
+
 /* Library version (MXGG_VERSION of the build). */
 int mxgg_version(void);
 
@@ -67,12 +80,15 @@ int mxgg_device_supported(void);
  *   src        (rows, cols) of src_dtype, row stride ld_src elements
  *   elem_fmt   MXGG_FMT_E4M3 (q is (rows, cols) bytes, row stride ld_q) or
  *              MXGG_FMT_E2M1 (q is (rows, cols/2) packed bytes, row stride ld_q)
- *   scales     (rows, cols/32) bytes, row stride ld_s
+ *   scales     scale_layout MXGG_SCALES_PLAIN: (rows, cols/32) bytes, row stride
+ *              ld_s.  MXGG_SCALES_STEPS: step-major for batches of ld_s rows
+ *              (ld_s divides rows; e.g. ld_s = N for an (E, N, K) weight
+ *              given as E*N rows), 4 * rows * ceil(cols/128) bytes.
  * cols must be a multiple of 32.
  */
 int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
                      int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
-                     uint8_t* scales, int64_t ld_s, void* stream);
+                     uint8_t* scales, int64_t ld_s, int scale_layout, void* stream);
 
 /*
  * MX quantization along dimension 0 with a transposed output: the result is
@@ -80,11 +96,12 @@ int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
  * weight gradient takes (kernels/backward.py:232-243).
  *   src     (rows, cols) of src_dtype, row stride ld_src; rows % 32 == 0
  *   q       (cols, rows) e4m3 bytes, row stride ld_q (elem_fmt must be E4M3)
- *   scales  (cols, rows/32) bytes, row stride ld_s
+ *   scales  MXGG_SCALES_PLAIN: (cols, rows/32) bytes, row stride ld_s;
+ *           MXGG_SCALES_STEPS: step-major [ceil(rows/128)][cols] dwords (ld_s = cols)
  */
 int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t cols,
                           int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
-                          uint8_t* scales, int64_t ld_s, void* stream);
+                          uint8_t* scales, int64_t ld_s, int scale_layout, void* stream);
 
 /*
  * Both MX layouts from one read of src: q_rows / s_rows = to_mx(src) and
@@ -99,10 +116,13 @@ int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t 
  *   src     (batch, rows, cols) of src_dtype, row stride ld_src; rows % 32 == 0, cols % 32 == 0
  *   q_rows  (batch, rows, cols) e4m3, row stride ld_qr;  s_rows (batch, rows, cols/32), row stride ld_sr
  *   q_cols  (batch, cols, rows) e4m3, row stride ld_qc;  s_cols (batch, cols, rows/32), row stride ld_sc
+ *   scale_layout MXGG_SCALES_STEPS: s_rows is [batch][ceil(cols/128)][rows] and s_cols
+ *           [batch][ceil(rows/128)][cols] dwords (ld_sr = rows, ld_sc = cols)
  */
 int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
                           int64_t ld_src, void* q_rows, int64_t ld_qr, uint8_t* s_rows, int64_t ld_sr,
-                          void* q_cols, int64_t ld_qc, uint8_t* s_cols, int64_t ld_sc, void* stream);
+                          void* q_cols, int64_t ld_qc, uint8_t* s_cols, int64_t ld_sc, int scale_layout,
+                          void* stream);
 
 /*
  * Routing table of the grouped GEMM, in the reference's buffer format
@@ -185,6 +205,23 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
                     void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * mxgg_grouped_mm with step-major scales (MXGG_SCALES_STEPS, written so by the
+ * quantizers): A_ss [T][M] and B_ss [E][T][N] uint32, T = ceil(K/128).  The
+ * same GEMM launches without the per-call re-layout of plain scales (the
+ * reference pre-shuffles its scales on every call too, kernels/forward.py:
+ * 367-397, 528-550).  workspace / ws_bytes (may be null / 0): room for the
+ * fp32 partial tiles of a split last round; mxgg_grouped_mm_workspace_size()
+ * is always enough.  Results are bit-identical to mxgg_grouped_mm given a
+ * workspace with the same room after its scales.
+ */
+int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32_t* A_ss,
+                          const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint32_t* B_ss,
+                          const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                          void* out, int out_dtype, int64_t ldo,
+                          int block_m, int block_n, int group_m, int xcd_swizzle,
+                          void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * mxgg_grouped_mm without a workspace: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid allocation).  Same arguments,
@@ -230,6 +267,18 @@ int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t 
                const uint8_t* ia_t, int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias,
                const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
                void* out, int out_dtype, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * mxgg_wgrad with step-major scales: go_ss [T][N] and ia_ss [T][K] uint32,
+ * T = ceil(M/128) (mxgg_quantize_mx_dim0 / _both with MXGG_SCALES_STEPS), no
+ * re-layout.  workspace / ws_bytes (may be null / 0): room for the fp32
+ * partial tiles of tiles cut along the tokens; mxgg_wgrad_workspace_size() is
+ * always enough.  Bit-identical to mxgg_wgrad given the same room.
+ */
+int mxgg_wgrad_steps(const uint8_t* go_t, int64_t ld_go, const uint32_t* go_ss,
+                     const uint8_t* ia_t, int64_t ld_ia, const uint32_t* ia_ss,
+                     const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
+                     void* out, int out_dtype, void* workspace, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -205,6 +205,30 @@ def to_mx(x, src: str = "bf16", elem: str = "e4m3", block: int = BLOCK):
     return s.reshape(shp[:-1] + (shp[-1] // block,)), q
 
 
+def step_major(scales: np.ndarray) -> np.ndarray:
+    """Plain scales ``(..., R, nblk)`` (uint8) -> the build's step-major layout
+    ``(..., T, R)`` uint32, ``T = cdiv(nblk, 4)``: word ``[t, r]`` holds
+    blocks ``4t .. 4t+3`` of row r, block ``4t+j`` in byte j, bytes past nblk
+    127.  Not the reference's CDNA4 pre-shuffle (kernels/forward.py:367-397);
+    the layout the build's GEMM kernels read and its quantizers can write.
+    """
+    s = np.asarray(scales, dtype=np.uint8)
+    nblk = s.shape[-1]
+    T = -(-nblk // 4)
+    pad = np.full(s.shape[:-1] + (4 * T,), 127, dtype=np.uint8)
+    pad[..., :nblk] = s
+    words = pad.reshape(s.shape[:-1] + (T, 4)).astype(np.uint32)
+    w = words[..., 0] | (words[..., 1] << 8) | (words[..., 2] << 16) | (words[..., 3] << 24)
+    return np.swapaxes(w, -1, -2).copy()
+
+
+def plain_from_step_major(words: np.ndarray, nblk: int) -> np.ndarray:
+    """Inverse of ``step_major``: ``(..., T, R)`` uint32 -> ``(..., R, nblk)`` uint8."""
+    w = np.swapaxes(np.asarray(words, dtype=np.uint32), -1, -2)
+    b = np.stack([(w >> (8 * j)) & 0xFF for j in range(4)], axis=-1).astype(np.uint8)
+    return b.reshape(w.shape[:-1] + (4 * w.shape[-1],))[..., :nblk].copy()
+
+
 def dequant(q: np.ndarray, scales: np.ndarray, elem: str = "e4m3", block: int = BLOCK,
             dtype=np.float64) -> np.ndarray:
     """Dequantize along the last dim: value * 2**(s-127) (exact in fp32/fp64).
@@ -472,6 +496,8 @@ PINNING = {
     "generate_jagged_offs": "invariants (sorted, distinct, multiples, last=M) and errors",
     "routing_table": "hand-derived KAT (E=4, offs=[96,352,640,1024], BM=128) plus brute force",
     "xcd_swizzle/pid_grid": "KAT (D=10, X=8) and bijection over many domains",
+    "step_major": "hand KAT (3 rows x 5 blocks: word values and 127 padding); exact inverse "
+                  "plain_from_step_major on random scales of many shapes",
     "band_tile/fwd_tile_order": "hand-derived KAT (E=4, offs=[96,352,640,1024], BM=BN=128, N=256, "
                                 "GROUP_M=2); brute force: every output element of every group covered "
                                 "by exactly one program, none past offs[-1]; equal to the reference's "

@@ -128,24 +128,37 @@ def test_wgrad_and_quant_validation_without_gpu():
     lib = _lib.load()
     rc = lib.mxgg_wgrad(16, 48, 16, 1, 16, 48, 16, 1, 16, 1, 48, 8, 8, 16, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"multiple of 32" in lib.mxgg_last_error_string()
-    rc = lib.mxgg_quantize_mx(16, 0, 4, 40, 40, 0, 16, 40, 16, 2, None)
+    rc = lib.mxgg_quantize_mx(16, 0, 4, 40, 40, 0, 16, 40, 16, 2, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"divisible by block_size 32" in lib.mxgg_last_error_string()
-    rc = lib.mxgg_quantize_mx(16, 5, 4, 64, 64, 0, 16, 64, 16, 2, None)
+    rc = lib.mxgg_quantize_mx(16, 5, 4, 64, 64, 0, 16, 64, 16, 2, 0, None)
     assert rc == _lib.ERR_INVALID_ARG
-    rc = lib.mxgg_quantize_mx_dim0(16, 0, 40, 64, 64, 0, 16, 40, 16, 1, None)
+    rc = lib.mxgg_quantize_mx_dim0(16, 0, 40, 64, 64, 0, 16, 40, 16, 1, 0, None)
     assert rc == _lib.ERR_INVALID_ARG
-    rc = lib.mxgg_quantize_mx_dim0(16, 0, 64, 64, 64, 4, 16, 64, 16, 2, None)
+    rc = lib.mxgg_quantize_mx_dim0(16, 0, 64, 64, 64, 4, 16, 64, 16, 2, 0, None)
     assert rc == _lib.ERR_UNSUPPORTED
     # empty problems are valid no-ops that never reach the device
-    assert lib.mxgg_quantize_mx(None, 0, 0, 64, 64, 0, None, 64, None, 2, None) == 0
+    assert lib.mxgg_quantize_mx(None, 0, 0, 64, 64, 0, None, 64, None, 2, 0, None) == 0
     # both-ways quantizer: both dims must be multiples of 32, strides cover the rows
-    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 40, 64, 64, 16, 64, 16, 2, 16, 40, 16, 1, None)
+    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 40, 64, 64, 16, 64, 16, 2, 16, 40, 16, 1, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"divisible by block_size 32" in lib.mxgg_last_error_string()
-    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 64, 64, 64, 16, 64, 16, 2, 16, 32, 16, 2, None)
+    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 64, 64, 64, 16, 64, 16, 2, 16, 32, 16, 2, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"stride" in lib.mxgg_last_error_string()
-    rc = lib.mxgg_quantize_mx_both(16, 7, 1, 64, 64, 64, 16, 64, 16, 2, 16, 64, 16, 2, None)
+    rc = lib.mxgg_quantize_mx_both(16, 7, 1, 64, 64, 64, 16, 64, 16, 2, 16, 64, 16, 2, 0, None)
     assert rc == _lib.ERR_INVALID_ARG
-    assert lib.mxgg_quantize_mx_both(None, 0, 0, 64, 64, 64, None, 64, None, 2, None, 64, None, 2, None) == 0
+    assert lib.mxgg_quantize_mx_both(None, 0, 0, 64, 64, 64, None, 64, None, 2, None, 64, None, 2, 0, None) == 0
+    # step-major scales: ld_s is the rows per batch and must divide the rows; unknown layout codes fail
+    rc = lib.mxgg_quantize_mx(16, 0, 6, 64, 64, 0, 16, 64, 16, 4, _lib.SCALES_STEPS, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"rows per batch" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_quantize_mx(16, 0, 6, 64, 64, 0, 16, 64, 16, 2, 9, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"scale_layout" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_quantize_mx_dim0(16, 0, 64, 96, 96, 0, 16, 64, 16, 64, _lib.SCALES_STEPS, None)
+    assert rc == _lib.ERR_INVALID_ARG
+    # GEMMs on step-major scales: scale words must be 4-byte aligned; wgrad still needs M % 32 == 0
+    rc = lib.mxgg_grouped_mm_steps(16, 64, 18, 16, 0, 64, 64 * 64, 16, 16, 1, 64, 64, 64,
+                                   16, 0, 64, 0, 0, 0, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"aligned" in lib.mxgg_last_error_string()
+    rc = lib.mxgg_wgrad_steps(16, 48, 16, 16, 48, 16, 16, 1, 48, 8, 8, 16, 0, None, 0, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 32" in lib.mxgg_last_error_string()
 
 
 def test_import_surface_matches_reference():
@@ -182,8 +195,12 @@ def test_wgrad_signature_matches_reference():
 def test_to_mx_signature_matches_reference():
     import utils
     sig = inspect.signature(utils.to_mx)
-    assert list(sig.parameters) == ["data", "elem_dtype", "block_size"]
+    # the reference's parameters in its order; additions are keyword-only with defaults
+    pos = [n for n, p in sig.parameters.items() if p.kind != p.KEYWORD_ONLY]
+    assert pos == ["data", "elem_dtype", "block_size"]
     assert sig.parameters["block_size"].default == 32
+    extra = [p for p in sig.parameters.values() if p.kind == p.KEYWORD_ONLY]
+    assert [p.name for p in extra] == ["scale_layout"] and extra[0].default == "plain"
 
 
 def test_cpu_tensors_fail_loudly():

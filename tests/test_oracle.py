@@ -355,6 +355,21 @@ def test_fwd_tile_order_reduces_to_reference_map():
                 assert (got[pid, 0], got[pid, 1]) == (e, starts[e] + b * BM)
 
 
+def test_step_major_kat_and_inverse():
+    s = np.arange(15, dtype=np.uint8).reshape(3, 5) + 100      # rows 0..2, blocks 0..4
+    w = O.step_major(s)
+    assert w.shape == (2, 3) and w.dtype == np.uint32
+    # row 1: blocks 105..109 -> word 0 = 105 | 106<<8 | 107<<16 | 108<<24, word 1 = 109 | 127 127 127
+    assert int(w[0, 1]) == 105 | 106 << 8 | 107 << 16 | 108 << 24
+    assert int(w[1, 1]) == 109 | 127 << 8 | 127 << 16 | 127 << 24
+    rng = np.random.default_rng(3)
+    for shape in ((1, 4), (7, 8), (2, 5, 13), (3, 64, 520)):
+        x = rng.integers(0, 255, size=shape, dtype=np.uint8)
+        ws = O.step_major(x)
+        assert ws.shape == shape[:-2] + (-(-shape[-1] // 4), shape[-2])
+        np.testing.assert_array_equal(O.plain_from_step_major(ws, shape[-1]), x)
+
+
 # ---------------------------------------------------------------- grouped GEMMs
 
 
