@@ -14,10 +14,18 @@ on the unquantized operands (reference bench.py:159-161) for the speedup the
 reference's README quotes (1.389x geomean MXFP8 vs bf16, README.md:80).
 
 Timed region per shape: the full drop-in Python call (output allocation, the
-C-ABI call, the in-kernel routing and the GEMM), bracketed by HIP events on
-the current stream after a 512 MB cache flush; median over ``--steps`` reps
-after ``--warmup`` reps.  TFLOPs = 2*M*N*K / t (bench.py:200).  A "step" is one
-call per shape over all 108 problems; ms_per_step is the sum of the medians.
+C-ABI call, the scale re-layout, the in-kernel routing and the GEMM),
+bracketed by HIP events on the current stream after a 512 MB cache flush;
+median over ``--steps`` reps after ``--warmup`` reps.  TFLOPs = 2*M*N*K / t
+(bench.py:200).  A "step" is one call per shape over all 108 problems;
+ms_per_step is the sum of the medians.
+
+Beside it, each call is timed again on step-major scales (the layout the
+kernels read, so the call launches no re-layout): between its events lie
+only the GEMM launches of the call (the whole-tile kernel, and the piece /
+quarter-tile / reduce launches when its last round is split).  The roofline
+of the dominant kernel uses that time.  Also measured
+(e4m3 x e2m1, E=8, M=16640, N=8192, K=5120) and the quantizer in GB/s.
 
 Prints ONE JSON line on stdout; progress and the per-shape table go to stderr
 and to gpurun_out/bench_detail.json when that directory exists.
@@ -40,8 +48,11 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "grouped-gemms_amd"))
 
 PEAK_MXFP8_TFLOPS = 5000.0          # MI355X published dense MXFP8 / FP8 peak
+PEAK_MXFP4_TFLOPS = 10100.0         # MI355X published dense MXFP4 peak
+PEAK_HBM_GBS = 8000.0               # MI355X HBM3E
 REF_FWD_GEOMEAN_TFLOPS = 1498.8     # reference README table, 36-shape fwd geomean (MI355X)
 REF_SPEEDUP_VS_BF16 = 1.389         # reference README, geomean MXFP8 / bf16 torch._grouped_mm (MI355X)
+REF_BF16_GEOMEAN_TFLOPS = 1079.0    # reference README table, bf16 torch._grouped_mm geomean (MI355X)
 M_TOKENS = 16640
 SHAPES = [(e, n, k) for e, n, k in itertools.product((1, 2, 4, 8), (2048, 5120, 8192), (2048, 5120, 8192))]
 
@@ -70,9 +81,9 @@ def time_call(fn, steps: int, warmup: int, flush_buf):
 def fwd_kernel_name(cfg: dict) -> str:
     """Device-kernel name (as rocprofv3 lists it) of the whole-tile kernel of an
     e4m3 forward/dgrad launch: Cfg<BLOCK_M, BLOCK_N, waves along M, waves along
-    N, B format, LDS stages>, pieces=false.  A call may also launch the piece
-    and reduce kernels of a split last round; bench.py's event time covers
-    the whole call."""
+    N, B format, LDS stages>, pieces=false, bf16 epilogue.  A call may also
+    launch the piece / quarter-tile / reduce kernels of a split last round;
+    the kernel-only event time covers those too."""
     return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4>, false, 1>"
 
 
@@ -209,10 +220,59 @@ def counter_summary(csv_path: str) -> str:
     return "\n".join(out)
 
 
-def stats_summary(stats_csv: str, bench_json: str) -> str:
+GEMM_KERNELS = ("mxgg::fwd_kernel<", "mxgg::fwd_quad_kernel<", "mxgg::fwd_reduce_kernel<", "mxgg::wgrad_kernel<",
+                "mxgg::wgrad_reduce_kernel<")
+
+
+def call_spans(trace_csv: str):
+    """GEMM calls in a ``rocprofv3 --kernel-trace`` CSV: each run of
+    consecutive GEMM dispatches that starts with a whole-tile kernel (between
+    the bench's cache flush, scale re-layout or quantizer kernels) is one
+    call.  Returns {whole-tile kernel of the call: [(span ns, cold), ...]},
+    span = last end - first start (what the bench's kernel-only events
+    bracket); cold: the call directly follows the 512 MB cache flush (a torch
+    fill kernel), as the bench's timed kernel-only reps do (its warmup reps
+    and the drop-in calls, whose re-layout sits in between, do not)."""
+    import csv
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                  for r in csv.DictReader(open(trace_csv)))
+    spans, cur, prev = {}, None, ""
+
+    def close():
+        if cur is not None and cur[2]:
+            spans.setdefault(cur[2], []).append((cur[1] - cur[0], cur[3]))
+        elif cur is not None and cur[4]:
+            # every tile of the call split: pieces and reduce only, counted with
+            # the whole-tile kernel of the same configuration (as the bench does)
+            spans.setdefault(cur[4], []).append((cur[1] - cur[0], cur[3]))
+
+    for t0, t1, name in rows:
+        n = name.replace("void ", "").split("(")[0]
+        if any(n.startswith(g) for g in GEMM_KERNELS):
+            whole = ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n
+            if cur is not None and whole and cur[2]:
+                close()          # back-to-back calls: a call's whole-tile kernel comes first
+                cur = None
+            if cur is None:
+                cur = [t0, t1, None, "FillFunctor" in prev, None]
+            cur[1] = max(cur[1], t1)
+            if whole:
+                cur[2] = n
+            elif ", true, 0>" in n and ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n):
+                cur[4] = n.replace(", true, 0>", ", false, 1>")
+        else:
+            close()
+            cur = None
+        prev = n if not any(n.startswith(g) for g in GEMM_KERNELS) else prev
+    close()
+    return spans
+
+
+def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str:
     """Per-kernel table of a ``rocprofv3 --kernel-trace --stats`` run over the
-    default bench (its ``*_kernel_stats.csv``), followed by the same run's own
-    HIP-event figures per GEMM kernel (the JSON line bench.py printed)."""
+    default bench (its ``*_kernel_stats.csv``), the per-call GEMM spans from
+    its kernel trace when given, and the same run's own HIP-event figures per
+    GEMM kernel (the JSON line bench.py printed)."""
     import csv
     out = [f"{'kernel':78s} {'calls':>6s} {'total ms':>9s} {'avg us':>9s} {'min us':>8s} {'max us':>8s} {'%':>6s}"]
     for r in csv.DictReader(open(stats_csv)):
@@ -224,6 +284,14 @@ def stats_summary(stats_csv: str, bench_json: str) -> str:
     for text in open(bench_json):
         if text.startswith("{"):
             line = json.loads(text)
+    if trace_csv:
+        out += ["", "Per call, from the kernel trace: the span of each call's GEMM dispatches (whole-tile kernel "
+                    "and any split / quarter-tile / reduce launches), by the call's whole-tile kernel:"]
+        for name, v in sorted(call_spans(trace_csv).items()):
+            cold = [t for t, c in v if c]
+            out.append(f"  {name:62s} all calls {len(v):6d}: avg {sum(t for t, _ in v) / len(v) / 1e3:9.2f} us;  "
+                       f"right after the cache flush {len(cold):6d}: avg "
+                       f"{(sum(cold) / len(cold) / 1e3) if cold else float('nan'):9.2f} us")
     if line and line.get("roofline"):
         rf = line["roofline"]
         out += ["", "Same run, bench.py's own figures (HIP events on the launch stream, timed reps only):"]
@@ -231,7 +299,7 @@ def stats_summary(stats_csv: str, bench_json: str) -> str:
             out.append(f"  {name:58s} avg {v['avg_launch_us']:9.2f} us over {v['launches']:5d} launches, "
                        f"{v['tflops']:7.1f} TFLOP/s")
         out.append(f"  dominant kernel {rf['kernel']}: achieved {rf['achieved']} TFLOP/s = {rf['frac']} of "
-                   f"{rf['peak']} (dense MXFP8)")
+                   f"{rf['peak']} (dense MXFP8), {rf['avg_launch_us']} us per call ({rf.get('scope', '')})")
         out.append(f"  headline: fwd geomean {line['fwd_geomean_tflops']}  dgrad {line['dgrad_geomean_tflops']}  "
                    f"wgrad {line['wgrad_geomean_tflops']} TFLOP/s")
     return "\n".join(out)
@@ -276,6 +344,55 @@ def cpu_baseline(budget_s: float):
                       f"cpu={platform.processor() or platform.machine()}"}
 
 
+def extra_measurements(dev, args, flush):
+    """BASELINE config 5 (MXFP8 x MXFP4 forward, E=8, M=16640, N=8192,
+    K=5120, offsets drawn with random.seed(4)) as a drop-in call and as
+    kernel-only time, and the quantizer's bandwidth on the sweep's largest
+    activation (16640 x 8192 bf16): to_mx (2 + 1 + 1/32 B per element),
+    to_mx_dim0 (the same bytes, transposed output) and to_mx_both (both
+    layouts from one read: 2 + 2 * (1 + 1/32) B per element)."""
+    import torch
+    from kernels import to_mx, to_mx_both, to_mx_dim0, triton_mxfp8_grouped_mm
+    from utils import generate_jagged_offs
+    M, E, N, K = M_TOKENS, 8, 8192, 5120
+    random.seed(4)
+    offs = generate_jagged_offs(E, M, multiple_of=32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(4)
+    a = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn((E, N, K), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    fp4 = torch.float4_e2m1fn_x2
+    sa, qa = to_mx(a)
+    sw, qw = to_mx(w, elem_dtype=fp4)
+    ta, _ = to_mx(a, scale_layout="steps")
+    tw, _ = to_mx(w, elem_dtype=fp4, scale_layout="steps")
+    del a, w
+    flops = 2.0 * M * N * K
+    med, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs), args.steps, args.warmup, flush)
+    kmed, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs), args.steps, args.warmup, flush)
+    tf = flops / (med * 1e-3) / 1e12
+    cfg5 = {"workload": "BASELINE config 5: e4m3 activations x e2m1 weights, E=8, M=16640, N=8192, K=5120, "
+                        "offs random.seed(4)",
+            "us": round(med * 1e3, 1), "tflops": round(tf, 1),
+            "frac_of_mxfp4_peak": round(tf / PEAK_MXFP4_TFLOPS, 4), "frac_of_mxfp8_peak": round(tf / PEAK_MXFP8_TFLOPS, 4),
+            "kernel_only_us": round(kmed * 1e3, 1), "kernel_only_tflops": round(flops / (kmed * 1e-3) / 1e12, 1)}
+    del qa, qw, sa, sw, ta, tw
+    torch.cuda.empty_cache()
+    x = torch.randn((M, 8192), device=dev).to(torch.bfloat16)
+    n = x.numel()
+    quant = {"workload": "bf16 (16640, 8192) -> e4m3 + e8m0 per 32, FLOOR scales (utils.py:67-105)"}
+    for name, fn, bpe in (("to_mx", lambda: to_mx(x), 2 + 1 + 1 / 32),
+                          ("to_mx_dim0", lambda: to_mx_dim0(x), 2 + 1 + 1 / 32),
+                          ("to_mx_both", lambda: to_mx_both(x), 2 + 2 * (1 + 1 / 32))):
+        qmed, _ = time_call(fn, args.steps, args.warmup, flush)
+        gbs = n * bpe / (qmed * 1e-3) / 1e9
+        quant[name] = {"us": round(qmed * 1e3, 1), "bytes_per_elem": round(bpe, 4), "gb_s": round(gbs, 1),
+                       "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    del x
+    torch.cuda.empty_cache()
+    log(json.dumps({"cfg5": cfg5, "quant": quant}))
+    return {"cfg5": cfg5, "quant": quant}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -287,6 +404,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-bf16", action="store_true",
                     help="skip the bf16 torch._grouped_mm arm of the forward (reference bench.py:159-161)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the BASELINE config 5 (e4m3 x e2m1) and quantizer measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 256 MiB device copies (PMC byte-counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -295,9 +414,10 @@ def main():
                          "and exit; runs on the CPU")
     ap.add_argument("--counter-summary", metavar="COUNTER_CSV",
                     help="per-kernel means of a rocprofv3 --pmc counter CSV and exit; runs on the CPU")
-    ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "BENCH_JSON"),
-                    help="summarize a rocprofv3 --kernel-trace --stats run of the default bench "
-                         "(its kernel_stats.csv and the JSON line it printed) and exit; runs on the CPU")
+    ap.add_argument("--stats-summary", nargs="+", metavar="CSV",
+                    help="STATS_CSV BENCH_JSON [TRACE_CSV]: summarize a rocprofv3 --kernel-trace --stats run of "
+                         "the default bench (its kernel_stats.csv, the JSON line it printed and, optionally, its "
+                         "kernel_trace.csv) and exit; runs on the CPU")
     args = ap.parse_args()
     if args.counter_summary:
         print(counter_summary(args.counter_summary))
@@ -341,6 +461,13 @@ def main():
         k["launches"] += args.steps
 
     t_start = time.time()
+    def kernel_only(key, fn, kernel, flops, row):
+        """Time the same call on step-major scales (only its GEMM launches lie
+        between the events) and account it to `kernel`'s roofline."""
+        kmed, kmean = time_call(fn, args.steps, args.warmup, flush)
+        row[key] = kmed * 1e3
+        account(kernel, kmean, flops)
+
     for (E, N, K) in shapes:
         M = M_TOKENS
         offs = offs_by_shape[(E, N, K)]
@@ -351,10 +478,14 @@ def main():
             w = (torch.randn((E, N, K), device=dev) * 0.02).to(torch.bfloat16)
             sa, qa = to_mx(a)
             sw, qw = to_mx(w)
+            ta, _ = to_mx(a, scale_layout="steps")
+            tw, _ = to_mx(w, scale_layout="steps")
             if not args.no_bf16:
                 # bf16 arm: torch's grouped GEMM on the unquantized operands, as the
-                # reference's bench does (bench.py:159-161); weights given as a
-                # contiguous (E, K, N) tensor rather than a transposed view
+                # reference's bench does (bench.py:159-161), but with the weight as a
+                # contiguous (E, K, N) tensor: the reference passes a transposed view
+                # of (E, N, K), and transposed right operands of torch's bf16 batched
+                # products have faulted GPUs of this pool
                 wk = w.transpose(-2, -1).contiguous()
                 bmed, _ = time_call(lambda: torch._grouped_mm(a, wk, offs, out_dtype=torch.bfloat16),
                                     args.steps, args.warmup, flush)
@@ -368,35 +499,43 @@ def main():
             row["fwd_tflops"] = flops / (med * 1e-3) / 1e12
             if "bf16_us" in row:
                 row["fwd_speedup_vs_bf16"] = row["bf16_us"] / row["fwd_us"]
-            account(fwd_kernel_name(_pick_config(E, M, N, K)), mean, flops)
-            del qa, qw, sa, sw
+            kernel_only("fwd_kernel_us", lambda: triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs),
+                        fwd_kernel_name(_pick_config(E, M, N, K)), flops, row)
+            del qa, qw, sa, sw, ta, tw
         if args.only in ("all", "dgrad"):
             go = torch.randn((M, N), device=dev).to(torch.bfloat16)
             wt = (torch.randn((E, K, N), device=dev) * 0.02).to(torch.bfloat16)   # W^T (E,K,N)
             sg, qg = to_mx(go)
             st_, qt = to_mx(wt)
+            tg, _ = to_mx(go, scale_layout="steps")
+            tt, _ = to_mx(wt, scale_layout="steps")
             del go, wt
             med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qg, qt, sg, st_, offs),
                                   args.steps, args.warmup, flush)
             row["dgrad_us"] = med * 1e3
             row["dgrad_tflops"] = flops / (med * 1e-3) / 1e12
-            account(fwd_kernel_name(_pick_config(E, M, K, N)), mean, flops)
-            del qg, qt, sg, st_
+            kernel_only("dgrad_kernel_us", lambda: triton_mxfp8_grouped_mm(qg, qt, tg, tt, offs),
+                        fwd_kernel_name(_pick_config(E, M, K, N)), flops, row)
+            del qg, qt, sg, st_, tg, tt
         if args.only in ("all", "wgrad"):
             go = torch.randn((M, N), device=dev).to(torch.bfloat16)
             ia = torch.randn((M, K), device=dev).to(torch.bfloat16)
             sg, qg = to_mx_dim0(go)          # (N, M)
             si, qi = to_mx_dim0(ia)          # (K, M)
+            tg, _ = to_mx_dim0(go, scale_layout="steps")
+            ti, _ = to_mx_dim0(ia, scale_layout="steps")
             del go, ia
             med, mean = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs),
                                   args.steps, args.warmup, flush)
             row["wgrad_us"] = med * 1e3
             row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
-            account(WGRAD_KERNEL, mean, flops)
-            del qg, qi, sg, si
+            kernel_only("wgrad_kernel_us", lambda: triton_mxfp8_wgrad(qg, tg, qi, ti, offs), WGRAD_KERNEL, flops, row)
+            del qg, qi, sg, si, tg, ti
         torch.cuda.empty_cache()
         rows.append(row)
         log(json.dumps({k: (round(v, 1) if isinstance(v, float) else v) for k, v in row.items()}))
+
+    extra = None if args.no_extra else extra_measurements(dev, args, flush)
 
     def gm(key):
         vals = [r[key] for r in rows if key in r]
@@ -412,7 +551,9 @@ def main():
             per_e[str(e)] = round(geomean(v), 1)
 
     # roofline of the dominant device kernel (largest summed time over the timed
-    # reps): algorithmic FLOPs 2*M*N*K per launch / its mean launch duration
+    # reps): algorithmic FLOPs 2*M*N*K per call / the mean time of the call's
+    # GEMM launches on step-major scales (HIP events on the launch stream; no
+    # re-layout launch between them, the split / quarter-tile tails included)
     roofline = None
     if kstats:
         kname, k = max(kstats.items(), key=lambda kv: kv[1]["ms"])
@@ -420,6 +561,8 @@ def main():
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MXFP8_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4),
                     "traffic": read_traffic(kname), "kernel": kname,
+                    "scope": "GEMM launches of one call on step-major scales: the whole-tile kernel, plus the "
+                             "piece / quarter-tile / reduce launches of a split last round",
                     "avg_launch_us": round(k["ms"] / k["launches"] * 1e3, 2),
                     "flops_per_launch": round(k["flops"] / k["launches"]),
                     "launches": k["launches"],
@@ -450,8 +593,19 @@ def main():
         "wgrad_geomean_tflops": round(wgrad_gm, 1) if wgrad_gm else None,
         "fwd_pct_of_peak": round(100 * fwd_gm / PEAK_MXFP8_TFLOPS, 2) if fwd_gm else None,
         "bf16_fwd_geomean_tflops": round(bf16_gm, 1) if bf16_gm else None,
+        "bf16_arm": "torch._grouped_mm on the unquantized operands, weight as a contiguous (E, K, N) tensor "
+                    "(the reference times a transposed (E, N, K) view, not run here), so the same-run speedup "
+                    "below is not the README's; fwd_speedup_vs_readme_bf16 divides by the README's own bf16 "
+                    "geomean (1079 TFLOP/s, MI355X)",
         "fwd_speedup_vs_bf16_geomean": round(speedup_gm, 3) if speedup_gm else None,
+        "fwd_speedup_vs_readme_bf16": round(fwd_gm / REF_BF16_GEOMEAN_TFLOPS, 3) if fwd_gm else None,
         "ref_speedup_vs_bf16_geomean": REF_SPEEDUP_VS_BF16,
+        "kernel_only_geomean_tflops": {d: (round(geomean([r["M"] * 2.0 * r["N"] * r["K"] / (r[d + "_kernel_us"] * 1e-6)
+                                                          / 1e12 for r in rows]), 1)
+                                           if rows and all(d + "_kernel_us" in r for r in rows) else None)
+                                       for d in ("fwd", "dgrad", "wgrad")},
+        "cfg5_mxfp4": extra["cfg5"] if extra else None,
+        "quantizer": extra["quant"] if extra else None,
         "fwd_geomean_by_E": per_e,
         "baseline_note": "vs_baseline = fwd geomean / 1498.8 TFLOP/s (reference README table, MI355X)",
         "roofline": roofline,
