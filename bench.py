@@ -379,14 +379,23 @@ def extra_measurements(dev, args, flush):
     torch.cuda.empty_cache()
     x = torch.randn((M, 8192), device=dev).to(torch.bfloat16)
     n = x.numel()
-    quant = {"workload": "bf16 (16640, 8192) -> e4m3 + e8m0 per 32, FLOOR scales (utils.py:67-105)"}
+    # what a plain device copy of the same tensor reaches under the same cache
+    # flush (the zeroed flush buffer's dirty lines drain during every timed rep)
+    y = torch.empty_like(x)
+    cmed, _ = time_call(lambda: y.copy_(x), args.steps, args.warmup, flush)
+    copy_gbs = 2 * x.numel() * x.element_size() / (cmed * 1e-3) / 1e9
+    del y
+    quant = {"workload": "bf16 (16640, 8192) -> e4m3 + e8m0 per 32, FLOOR scales (utils.py:67-105)",
+             "copy_reference": {"us": round(cmed * 1e3, 1), "gb_s": round(copy_gbs, 1),
+                                "what": "torch copy_ of the same bf16 tensor (read + write), same flush"}}
     for name, fn, bpe in (("to_mx", lambda: to_mx(x), 2 + 1 + 1 / 32),
                           ("to_mx_dim0", lambda: to_mx_dim0(x), 2 + 1 + 1 / 32),
                           ("to_mx_both", lambda: to_mx_both(x), 2 + 2 * (1 + 1 / 32))):
         qmed, _ = time_call(fn, args.steps, args.warmup, flush)
         gbs = n * bpe / (qmed * 1e-3) / 1e9
         quant[name] = {"us": round(qmed * 1e3, 1), "bytes_per_elem": round(bpe, 4), "gb_s": round(gbs, 1),
-                       "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+                       "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                       "frac_of_copy_rate": round(gbs / copy_gbs, 4)}
     del x
     torch.cuda.empty_cache()
     log(json.dumps({"cfg5": cfg5, "quant": quant}))

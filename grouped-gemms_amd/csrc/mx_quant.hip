@@ -2,19 +2,25 @@
 //
 // Row-wise kernel (`mxgg_quantize_mx`, the reference's `to_mx`, utils.py:67-105):
 // four lanes own one 32-element block (8 elements each), so a wave reads 16
-// consecutive blocks of a row with fully coalesced 16-byte loads, reduces the
-// block amax with two lane shuffles, and writes 8 e4m3 bytes (or 4 packed e2m1
-// bytes) per lane.  HBM-bound: 3.03 B/element for bf16 -> e4m3.
+// consecutive blocks of a row with fully coalesced 16-byte loads (four such
+// runs in flight), reduces the block amax with two lane shuffles, and writes 8
+// e4m3 bytes (or 4 packed e2m1 bytes) per lane.  HBM-bound: 3.03 B/element
+// for bf16 -> e4m3.
 //
 // Column-wise kernel (`mxgg_quantize_mx_dim0`, i.e. to_mx(x.t().contiguous())
 // used for the weight-gradient operands, kernels/backward.py:232-243): a
-// workgroup stages a 32-row x 256-column tile through LDS and each thread
-// quantizes one column block, writing the transposed row of the output.
+// workgroup stages a 128 x 128 tile through LDS and each thread quantizes
+// column blocks, so every line of the transposed output (128 source rows of
+// one column) is written whole by one workgroup.
 //
 // Both-ways kernel (`mxgg_quantize_mx_both`): the same tile also yields the
 // row-wise blocks, so one read of the source gives to_mx(x) and
 // to_mx(x.t().contiguous()): 2 + 2 * (1 + 1/32) = 4.06 bytes per bf16
 // element instead of 6.06 for the two passes.
+//
+// The e4m3 cast is the hardware fp8 conversion of the clamped, exactly
+// scaled value (round to nearest even); blocks holding a NaN take the
+// bit-level path, which keeps the NaN's sign as the reference's cast does.
 //
 // Scales go out in the reference's plain layout (row-major (rows, blocks)
 // bytes) or step-major, the layout the GEMM kernels read (MXGG_SCALES_STEPS:
@@ -48,6 +54,34 @@ __device__ __forceinline__ void put_scale(const ScaleOut& o, int64_t r, int64_t 
     for (int k = j + 1; k < 4; ++k) d[k] = 127;
 }
 
+// Scale bytes of blocks blk0 .. blk0+n-1 of global row r (blk0 % 4 == 0,
+// 1 <= n <= 4; byte j of w for block blk0 + j), from one lane: one dword
+// store where the layout allows it.  n < 4 only where the row ends, so in the
+// step-major layout the bytes past n are the neutral 127.
+__device__ __forceinline__ void put_scale4(const ScaleOut& o, int64_t r, int64_t blk0, uint32_t w, int n) {
+  if (o.steps) {
+    if (n < 4) w = (w & ((1u << (8 * n)) - 1u)) | (0x7f7f7f7fu << (8 * n));
+    const int64_t b = r / o.ld, rr = r - b * o.ld;
+    *reinterpret_cast<uint32_t*>(o.p + ((b * o.T + (blk0 >> 2)) * o.ld + rr) * 4) = w;
+    return;
+  }
+  uint8_t* d = o.p + r * o.ld + blk0;
+  if (n == 4 && ((uintptr_t)d & 3) == 0) {
+    *reinterpret_cast<uint32_t*>(d) = w;
+    return;
+  }
+  for (int j = 0; j < n; ++j) d[j] = (uint8_t)(w >> (8 * j));
+}
+
+// The 4 scale bytes of a group of four consecutive lanes (lane j of the
+// group holds block j's byte s), gathered into every lane of the group.
+__device__ __forceinline__ uint32_t gather4(uint32_t s, int j) {
+  uint32_t v = s << (8 * j);
+  v |= (uint32_t)__shfl_xor((int)v, 1, 4);
+  v |= (uint32_t)__shfl_xor((int)v, 2, 4);
+  return v;
+}
+
 template <int SRC>
 __device__ __forceinline__ void load8(const uint8_t* p, float (&v)[8]) {
   if constexpr (SRC == MXGG_DTYPE_BF16) {
@@ -78,190 +112,233 @@ constexpr int elem_bytes() {
   return SRC == MXGG_DTYPE_F32 ? 4 : 2;
 }
 
-// One quad of lanes per block; grid-stride over all (row, block) pairs.
-template <int SRC, int FMT>
+template <int SRC>
+__device__ __forceinline__ float elem_to_f32(const uint8_t* p) {
+  if constexpr (SRC == MXGG_DTYPE_BF16) return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+  else if constexpr (SRC == MXGG_DTYPE_F16) return (float)*reinterpret_cast<const _Float16*>(p);
+  else return *reinterpret_cast<const float*>(p);
+}
+
+// e4m3 codes of a, b, c, d (bytes 0..3): clamp(x * mul, -448, 448) rounded
+// to nearest even by the hardware fp8 conversion -- the bytes of the
+// reference's clamp-then-cast (utils.py:97-102) for every input but NaN,
+// which the caller routes to e4m3x4_sw.  mul is an exact power of two, inf
+// clamps to +-448 like the reference's clamp, and a product that is an fp32
+// subnormal rounds to a signed zero either way.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d, float mul) {
+  const float ya = __builtin_amdgcn_fmed3f(a * mul, -448.f, 448.f);
+  const float yb = __builtin_amdgcn_fmed3f(b * mul, -448.f, 448.f);
+  const float yc = __builtin_amdgcn_fmed3f(c * mul, -448.f, 448.f);
+  const float yd = __builtin_amdgcn_fmed3f(d * mul, -448.f, 448.f);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ya, yb, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(yc, yd, (int)lo, true);
+}
+
+// The same four codes by the bit-level conversion (any input, NaN included:
+// NaN keeps its sign, 0x7f / 0xff).
+__device__ __forceinline__ uint32_t e4m3x4_sw(float a, float b, float c, float d, float mul) {
+  return e4m3_code(a, mul) | (e4m3_code(b, mul) << 8) | (e4m3_code(c, mul) << 16) | (e4m3_code(d, mul) << 24);
+}
+
+// max |x| bit pattern of n fp32 values (NaN above inf, as the reference's amax
+// propagates NaN).
+template <int N>
+__device__ __forceinline__ uint32_t amax_bits(const float* v) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint32_t a = abs_bits(v[i]);
+    m = a > m ? a : m;
+  }
+  return m;
+}
+
+// One 32-element block held by one lane: FLOOR scale (returned), 32 e4m3
+// bytes at dst (16-byte aligned).
+__device__ __forceinline__ uint32_t quant32(const float (&v)[32], uint8_t* dst) {
+  const uint32_t m = amax_bits<32>(v);
+  const uint32_t sc = floor_scale(m, 8);
+  const float mul = inv_scale(sc);
+  uint32_t w[8];
+  if (m > 0x7f800000u) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = e4m3x4_sw(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], mul);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = e4m3x4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3], mul);
+  }
+  *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
+  return sc;
+}
+
+// Launch shape knobs (experiments override them with -D): the row kernel's
+// grid cap (0: one pass, a workgroup per 64 blocks) and a waves-per-SIMD hint
+// for the tile kernel (1: none).
+#ifndef MXGG_QROWS_CAP
+#define MXGG_QROWS_CAP 0
+#endif
+#ifndef MXGG_QTILE_WPE
+#define MXGG_QTILE_WPE 1
+#endif
+
+// Row-wise quantization: four lanes (a quad) own one 32-element block, 8
+// elements each; a workgroup's 64 quads take 64 consecutive blocks (a
+// contiguous 4 KB of bf16), one grid-stride pass per 64 * gridDim.x blocks.
+// When rows hold a multiple of 4 blocks, four consecutive quads' scale bytes
+// (one step of a row) go out as one dword.  I: the block index type (32-bit
+// when the block count fits: one cheap division per block).
+template <int SRC, int FMT, class I>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restrict__ src,
                                                          int64_t rows, int64_t cols,
                                                          int64_t ld_src_bytes,
                                                          uint8_t* __restrict__ q, int64_t ld_q,
                                                          ScaleOut so) {
-  const int64_t bpr = cols / 32;                       // blocks per row
-  const int64_t nblk = rows * bpr;
+  const I bpr = (I)(cols / 32);                        // blocks per row
+  const I nblk = (I)rows * bpr;
   const int sub = threadIdx.x & 3;                     // which 8 of the 32
-  const int64_t quads = (int64_t)gridDim.x * (blockDim.x / 4);
-  for (int64_t b = (int64_t)blockIdx.x * (blockDim.x / 4) + (threadIdx.x >> 2); b < nblk + 0;
-       b += quads) {
-    // all four lanes of a quad share b, so the quad stays together in the loop
-    const int64_t r = b / bpr;
-    const int64_t cb = b - r * bpr;
-    const int64_t col = cb * 32 + sub * 8;
-    float v[8];
-    load8<SRC>(src + r * ld_src_bytes + col * elem_bytes<SRC>(), v);
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t a = abs_bits(v[i]);
-      m = a > m ? a : m;
-    }
-    uint32_t m1 = (uint32_t)__shfl_xor((int)m, 1, 4);
+  const int qd = (threadIdx.x >> 2) & 3;               // quad within a group of four
+  const bool by4 = bpr % 4 == 0;
+  const I stride = (I)gridDim.x * 64;
+  for (I base = (I)blockIdx.x * 64; base < nblk; base += stride) {
+    // every lane of the wave runs each pass (the scale gathers are wave-wide);
+    // lanes of blocks past nblk load and store nothing
+    const I b = base + (I)(threadIdx.x >> 2);
+    const bool live = b < nblk;
+    const I r = live ? b / bpr : 0;
+    const I cb = live ? b - r * bpr : 0;
+    const int64_t col = (int64_t)cb * 32 + sub * 8;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) load8<SRC>(src + (int64_t)r * ld_src_bytes + col * elem_bytes<SRC>(), v);
+    uint32_t m = amax_bits<8>(v);
+    const uint32_t m1 = (uint32_t)__shfl_xor((int)m, 1, 4);
     m = m1 > m ? m1 : m;
-    uint32_t m2 = (uint32_t)__shfl_xor((int)m, 2, 4);
+    const uint32_t m2 = (uint32_t)__shfl_xor((int)m, 2, 4);
     m = m2 > m ? m2 : m;
     const uint32_t s = floor_scale(m, FMT == MXGG_FMT_E4M3 ? 8 : 2);
     const float mul = inv_scale(s);
-    if constexpr (FMT == MXGG_FMT_E4M3) {
-      uint32_t lo = 0, hi = 0;
+    if (live) {
+      if constexpr (FMT == MXGG_FMT_E4M3) {
+        uint32_t lo, hi;
+        if (m > 0x7f800000u) {
+          lo = e4m3x4_sw(v[0], v[1], v[2], v[3], mul);
+          hi = e4m3x4_sw(v[4], v[5], v[6], v[7], mul);
+        } else {
+          lo = e4m3x4(v[0], v[1], v[2], v[3], mul);
+          hi = e4m3x4(v[4], v[5], v[6], v[7], mul);
+        }
+        *reinterpret_cast<uint2*>(q + (int64_t)r * ld_q + col) = make_uint2(lo, hi);
+      } else {
+        uint32_t w = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lo |= e4m3_code(v[i], mul) << (8 * i);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) hi |= e4m3_code(v[4 + i], mul) << (8 * i);
-      *reinterpret_cast<uint2*>(q + r * ld_q + col) = make_uint2(lo, hi);
-    } else {
-      uint32_t w = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) w |= e2m1_code(v[i], mul) << (4 * i);
-      *reinterpret_cast<uint32_t*>(q + r * ld_q + col / 2) = w;
+        for (int i = 0; i < 8; ++i) w |= e2m1_code(v[i], mul) << (4 * i);
+        *reinterpret_cast<uint32_t*>(q + (int64_t)r * ld_q + col / 2) = w;
+      }
     }
-    if (sub == 0) put_scale(so, r, cb, s);
+    if (by4) {
+      // quads 4k .. 4k+3 of a wave hold blocks 4k' .. 4k'+3 of one row (base
+      // is a multiple of 64, rows a multiple of 4 blocks)
+      uint32_t w4 = s << (8 * qd);
+      w4 |= (uint32_t)__shfl_xor((int)w4, 4, 16);
+      w4 |= (uint32_t)__shfl_xor((int)w4, 8, 16);
+      if (live && qd == 0 && sub == 0) {
+        const I left = nblk - b;
+        put_scale4(so, r, cb, w4, left < 4 ? (int)left : 4);
+      }
+    } else if (live && sub == 0) {
+      put_scale(so, r, cb, s);
+    }
   }
 }
 
-// Column-wise (dim-0) quantization with transposed output.  Tile: 32 source
-// rows x 256 source columns per workgroup (256 threads, one column each).
-template <int SRC>
-__global__ __launch_bounds__(256) void quant_cols_kernel(const uint8_t* __restrict__ src,
-                                                         int64_t rows, int64_t cols,
-                                                         int64_t ld_src_bytes,
-                                                         uint8_t* __restrict__ q, int64_t ld_q,
-                                                         ScaleOut so) {
+// Column-wise quantization with transposed output (to_mx of the transpose),
+// and with ROWS the row-wise quantization of the same data: one 128 x 128
+// source tile per workgroup (batch blockIdx.z) staged through LDS.  Four
+// consecutive lanes own the four 32-element blocks of one 128-element line of
+// an output -- a column of the tile (source rows 32j .. 32j+31 in lane j) or a
+// row of it (columns 32j .. 32j+31) -- so one store instruction writes whole
+// 128-byte output lines and the group's four scale bytes leave as one dword.
+// In LDS, 32-row band k of the tile is rotated by 16k columns, so the four
+// lanes of a group, reading four bands of one column, hit disjoint banks.
+// rows % 32 == 0: a partial last tile has whole 32-row blocks.
+template <int SRC, bool ROWS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MXGG_QTILE_WPE))) void quant_tile_kernel(
+    const uint8_t* __restrict__ src, int64_t rows, int64_t cols, int64_t ld_src_bytes, uint8_t* __restrict__ q_r,
+    int64_t ld_qr, ScaleOut s_r, uint8_t* __restrict__ q_c, int64_t ld_qc, ScaleOut s_c) {
   constexpr int EB = elem_bytes<SRC>();
-  constexpr int TC = 256;                         // tile columns
-  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * TC * EB];
-  const int64_t r0 = (int64_t)blockIdx.y * 32;
-  const int64_t c0 = (int64_t)blockIdx.x * TC;
-  const int t = threadIdx.x;
-  // cooperative 16-byte loads of the 32 x TC tile (columns past `cols` are
-  // left untouched and never read back)
-  constexpr int CHUNKS_PER_ROW = TC * EB / 16;
-  for (int i = t; i < 32 * CHUNKS_PER_ROW; i += 256) {
-    int rr = i / CHUNKS_PER_ROW;
-    int cc = i - rr * CHUNKS_PER_ROW;
-    int64_t col = c0 + (int64_t)cc * (16 / EB);
-    if (col < cols) {
-      uint4 u = *reinterpret_cast<const uint4*>(src + (r0 + rr) * ld_src_bytes + col * EB);
-      *reinterpret_cast<uint4*>(&tile[(rr * TC) * EB + cc * 16]) = u;
-    }
-  }
-  __syncthreads();
-  const int64_t col = c0 + t;
-  if (col >= cols) return;
-  float v[32];
-#pragma unroll
-  for (int rr = 0; rr < 32; ++rr) {
-    const uint8_t* p = &tile[(rr * TC + t) * EB];
-    if constexpr (SRC == MXGG_DTYPE_BF16) {
-      v[rr] = bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
-    } else if constexpr (SRC == MXGG_DTYPE_F16) {
-      v[rr] = (float)*reinterpret_cast<const _Float16*>(p);
-    } else {
-      v[rr] = *reinterpret_cast<const float*>(p);
-    }
-  }
-  uint32_t m = 0;
-#pragma unroll
-  for (int rr = 0; rr < 32; ++rr) {
-    uint32_t a = abs_bits(v[rr]);
-    m = a > m ? a : m;
-  }
-  const uint32_t s = floor_scale(m, 8);
-  const float mul = inv_scale(s);
-  uint32_t w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    w[i] = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[i] |= e4m3_code(v[4 * i + j], mul) << (8 * j);
-  }
-  uint8_t* dst = q + col * ld_q + r0;
-  *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-  *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-  put_scale(so, col, r0 / 32, s);
-}
-
-// Row-wise and column-wise quantization of one 32 x 256 tile of batch
-// blockIdx.z: thread t quantizes the row block (row t / 8, columns
-// 32 (t % 8) .. +31) and the column block (column t, the tile's 32 rows).
-template <int SRC>
-__global__ __launch_bounds__(256) void quant_both_kernel(const uint8_t* __restrict__ src,
-                                                         int64_t rows, int64_t cols,
-                                                         int64_t ld_src_bytes,
-                                                         uint8_t* __restrict__ q_r, int64_t ld_qr, ScaleOut s_r,
-                                                         uint8_t* __restrict__ q_c, int64_t ld_qc, ScaleOut s_c) {
-  constexpr int EB = elem_bytes<SRC>();
-  constexpr int TC = 256;
-  __shared__ __attribute__((aligned(16))) uint8_t tile[32 * TC * EB];
+  constexpr int T = 128;                              // tile rows and columns
+  constexpr int PITCH = T * EB + 16;                  // LDS row pitch, bytes
+  constexpr int EPC = 16 / EB;                        // elements per 16-byte chunk
+  constexpr int CPR = T / EPC;                        // chunks per tile row
+  constexpr int NCH = T * CPR / 256;                  // chunks per thread
+  __shared__ __attribute__((aligned(16))) uint8_t tile[T * PITCH];
+  // byte offset of element (r, c) of the tile
+  auto at = [](int r, int c) { return r * PITCH + (((c + 16 * (r >> 5)) & (T - 1)) * EB); };
   const int64_t b = blockIdx.z;
   src += b * rows * ld_src_bytes;
-  q_r += b * rows * ld_qr;
   q_c += b * cols * ld_qc;
-  const int64_t r0 = (int64_t)blockIdx.y * 32;
-  const int64_t c0 = (int64_t)blockIdx.x * TC;
+  if constexpr (ROWS) q_r += b * rows * ld_qr;
+  const int64_t r0 = (int64_t)blockIdx.y * T;
+  const int64_t c0 = (int64_t)blockIdx.x * T;
+  const int tr = (int)(rows - r0 < T ? rows - r0 : T);
+  const int tc = (int)(cols - c0 < T ? cols - c0 : T);
   const int t = threadIdx.x;
-  constexpr int CHUNKS_PER_ROW = TC * EB / 16;
-  for (int i = t; i < 32 * CHUNKS_PER_ROW; i += 256) {
-    int rr = i / CHUNKS_PER_ROW;
-    int cc = i - rr * CHUNKS_PER_ROW;
-    int64_t col = c0 + (int64_t)cc * (16 / EB);
-    if (col < cols) {
-      uint4 u = *reinterpret_cast<const uint4*>(src + (r0 + rr) * ld_src_bytes + col * EB);
-      *reinterpret_cast<uint4*>(&tile[(rr * TC) * EB + cc * 16]) = u;
+  {
+    uint4 u[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int idx = t + 256 * i;
+      const int rr = idx / CPR, c = (idx % CPR) * EPC;
+      u[i] = (rr < tr && c < tc) ? *reinterpret_cast<const uint4*>(src + (r0 + rr) * ld_src_bytes + (c0 + c) * EB)
+                                 : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<uint4*>(&tile[at(idx / CPR, (idx % CPR) * EPC)]) = u[i];
     }
   }
   __syncthreads();
-  auto load = [&](int rr, int cc) -> float {
-    const uint8_t* p = &tile[(rr * TC + cc) * EB];
-    if constexpr (SRC == MXGG_DTYPE_BF16) return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
-    else if constexpr (SRC == MXGG_DTYPE_F16) return (float)*reinterpret_cast<const _Float16*>(p);
-    else return *reinterpret_cast<const float*>(p);
-  };
-  // block blk of global row r (over every batch) of scale output so
-  auto quant32 = [&](const float (&v)[32], uint8_t* dst, const ScaleOut& so, int64_t r, int64_t blk) {
-    uint32_t m = 0;
+  const int j = t & 3;                                // block of the lane within its line
+  const int bands = tr / 32;                          // valid 32-row blocks of the tile
+  // columns: group g = t / 4 + 64 pass owns tile column g (output row c0 + g)
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      uint32_t a = abs_bits(v[i]);
-      m = a > m ? a : m;
-    }
-    const uint32_t sc = floor_scale(m, 8);
-    const float mul = inv_scale(sc);
-    uint32_t w[8];
+  for (int pass = 0; pass < 2; ++pass) {
+    const int c = t / 4 + 64 * pass;
+    if (c < tc) {                                     // uniform over the four lanes
+      uint32_t sc = 127;
+      if (j < bands) {
+        float v[32];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      w[i] = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w[i] |= e4m3_code(v[4 * i + j], mul) << (8 * j);
-    }
-    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-    *reinterpret_cast<uint4*>(dst + 16) = make_uint4(w[4], w[5], w[6], w[7]);
-    put_scale(so, r, blk, sc);
-  };
-  {
-    const int rr = t / 8, cb = t % 8;
-    const int64_t col0 = c0 + cb * 32;
-    if (col0 < cols) {                             // cols % 32 == 0: whole blocks
-      float v[32];
-#pragma unroll
-      for (int i = 0; i < 32; ++i) v[i] = load(rr, cb * 32 + i);
-      quant32(v, q_r + (r0 + rr) * ld_qr + col0, s_r, b * rows + r0 + rr, col0 / 32);
+        for (int i = 0; i < 32; ++i) v[i] = elem_to_f32<SRC>(&tile[at(32 * j + i, c)]);
+        sc = quant32(v, q_c + (c0 + c) * ld_qc + r0 + 32 * j);
+      }
+      const uint32_t w4 = gather4(sc, j);
+      if (j == 0) put_scale4(s_c, b * cols + c0 + c, r0 / 32, w4, bands < 4 ? bands : 4);
     }
   }
-  {
-    const int64_t col = c0 + t;
-    if (col < cols) {
-      float v[32];
+  if constexpr (ROWS) {
+    // rows: group g = t / 4 + 64 pass owns tile row g (output row r0 + g)
+    const int nb = tc / 32;                           // cols % 32 == 0
 #pragma unroll
-      for (int rr = 0; rr < 32; ++rr) v[rr] = load(rr, t);
-      quant32(v, q_c + col * ld_qc + r0, s_c, b * cols + col, r0 / 32);
+    for (int pass = 0; pass < 2; ++pass) {
+      const int r = t / 4 + 64 * pass;
+      if (r < tr) {
+        uint32_t sc = 127;
+        if (j < nb) {
+          float v[32];
+#pragma unroll
+          for (int k = 0; k < 32; k += EPC) {
+            const uint4 ch = *reinterpret_cast<const uint4*>(&tile[at(r, 32 * j + k)]);
+            const uint8_t* cp = reinterpret_cast<const uint8_t*>(&ch);
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) v[k + e] = elem_to_f32<SRC>(cp + e * EB);
+          }
+          sc = quant32(v, q_r + (r0 + r) * ld_qr + c0 + 32 * j);
+        }
+        const uint32_t w4 = gather4(sc, j);
+        if (j == 0) put_scale4(s_r, b * rows + r0 + r, c0 / 32, w4, nb < 4 ? nb : 4);
+      }
     }
   }
 }
@@ -318,14 +395,24 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: output rows misaligned");
   if (int rc = require_device()) return rc;
   const int64_t nblk = rows * (cols / 32);
-  int64_t want = (nblk + 63) / 64;                   // 64 blocks per 256-thread WG
-  const int grid = (int)(want < 65536 ? (want < 1 ? 1 : want) : 65536);
+  // 64 quads per 256-thread workgroup, one block each: one pass
+  const int64_t want = (nblk + 63) / 64;
+  const int64_t cap = MXGG_QROWS_CAP > 0 ? MXGG_QROWS_CAP : INT32_MAX;
+  const int grid = (int)(want < cap ? (want < 1 ? 1 : want) : cap);
   hipStream_t st = (hipStream_t)stream;
   const uint8_t* s8 = (const uint8_t*)src;
   uint8_t* q8 = (uint8_t*)q;
   const int64_t lsb = ld_src * eb;
-#define MXGG_QROWS(SRC, FMT) \
-  hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT>), dim3(grid), dim3(256), 0, st, s8, rows, cols, lsb, q8, ld_q, so)
+  const bool small = nblk + (int64_t)grid * 64 < ((int64_t)1 << 32);   // block indices fit 32 bits
+#define MXGG_QROWS(SRC, FMT)                                                                               \
+  do {                                                                                                     \
+    if (small)                                                                                             \
+      hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT, uint32_t>), dim3(grid), dim3(256), 0, st, s8, rows,  \
+                         cols, lsb, q8, ld_q, so);                                                         \
+    else                                                                                                   \
+      hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT, int64_t>), dim3(grid), dim3(256), 0, st, s8, rows,   \
+                         cols, lsb, q8, ld_q, so);                                                         \
+  } while (0)
   if (elem_fmt == MXGG_FMT_E4M3) {
     if (src_dtype == MXGG_DTYPE_BF16) MXGG_QROWS(MXGG_DTYPE_BF16, MXGG_FMT_E4M3);
     else if (src_dtype == MXGG_DTYPE_F16) MXGG_QROWS(MXGG_DTYPE_F16, MXGG_FMT_E4M3);
@@ -361,17 +448,19 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
   if (((uintptr_t)q % 16) || (ld_q % 16))
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: output rows must be 16-byte aligned");
   if (int rc = require_device()) return rc;
-  dim3 grid((unsigned)((cols + 255) / 256), (unsigned)(rows / 32));
+  dim3 grid((unsigned)((cols + 127) / 128), (unsigned)((rows + 127) / 128));
   if (grid.y > 65535u) return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx_dim0: too many rows");
   hipStream_t st = (hipStream_t)stream;
   const uint8_t* s8 = (const uint8_t*)src;
   const int64_t lsb = ld_src * eb;
-  if (src_dtype == MXGG_DTYPE_BF16)
-    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_BF16>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, so);
-  else if (src_dtype == MXGG_DTYPE_F16)
-    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F16>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, so);
-  else
-    hipLaunchKernelGGL(quant_cols_kernel<MXGG_DTYPE_F32>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q, ld_q, so);
+  const ScaleOut none{};
+#define MXGG_QCOLS(SRC) \
+  hipLaunchKernelGGL((quant_tile_kernel<SRC, false>), grid, dim3(256), 0, st, s8, rows, cols, lsb, nullptr, 0, none, \
+                     (uint8_t*)q, ld_q, so)
+  if (src_dtype == MXGG_DTYPE_BF16) MXGG_QCOLS(MXGG_DTYPE_BF16);
+  else if (src_dtype == MXGG_DTYPE_F16) MXGG_QCOLS(MXGG_DTYPE_F16);
+  else MXGG_QCOLS(MXGG_DTYPE_F32);
+#undef MXGG_QCOLS
   return launch_status("quantize_mx_dim0");
 }
 
@@ -400,14 +489,15 @@ extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t bat
   if (((uintptr_t)q_rows % 16) || (ld_qr % 16) || ((uintptr_t)q_cols % 16) || (ld_qc % 16))
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: output rows must be 16-byte aligned");
   if (int rc = require_device()) return rc;
-  dim3 grid((unsigned)((cols + 255) / 256), (unsigned)(rows / 32), (unsigned)batch);
-  if (rows / 32 > 65535 || batch > 65535) return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx_both: too many rows or batches");
+  dim3 grid((unsigned)((cols + 127) / 128), (unsigned)((rows + 127) / 128), (unsigned)batch);
+  if ((rows + 127) / 128 > 65535 || batch > 65535)
+    return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx_both: too many rows or batches");
   hipStream_t st = (hipStream_t)stream;
   const uint8_t* s8 = (const uint8_t*)src;
   const int64_t lsb = ld_src * eb;
 #define MXGG_QBOTH(SRC)                                                                                  \
-  hipLaunchKernelGGL(quant_both_kernel<SRC>, grid, dim3(256), 0, st, s8, rows, cols, lsb, (uint8_t*)q_rows, \
-                     ld_qr, sr, (uint8_t*)q_cols, ld_qc, sc)
+  hipLaunchKernelGGL((quant_tile_kernel<SRC, true>), grid, dim3(256), 0, st, s8, rows, cols, lsb,         \
+                     (uint8_t*)q_rows, ld_qr, sr, (uint8_t*)q_cols, ld_qc, sc)
   if (src_dtype == MXGG_DTYPE_BF16) MXGG_QBOTH(MXGG_DTYPE_BF16);
   else if (src_dtype == MXGG_DTYPE_F16) MXGG_QBOTH(MXGG_DTYPE_F16);
   else MXGG_QBOTH(MXGG_DTYPE_F32);
