@@ -1325,9 +1325,37 @@ __device__ __forceinline__ bool wgrad_split_tile(const WgradParams& p, int v, in
   return true;
 }
 
-// PIECES = false: grid (tiles_n * tiles_k, E), workgroup (x, g) computes tile
-// g * tiles_n * tiles_k + x whole when below wgrad_whole (epilogue EPI);
-// true: workgroup u computes the piece wgrad_unit assigns it.
+// Group of dispatch slot y of the whole-tile grid: the groups longest first
+// (most reduction steps; ties by index).  The hardware starts workgroups in
+// blockIdx order as CUs free up, so with more tiles than CUs this is the
+// longest-processing-time-first schedule: a long group's tiles start in the
+// first round instead of behind short groups (E=8, N=K=2048 with groups of 3
+// to 44 steps: a 44-step tile then bounds the launch, not a short round plus
+// a 36-step one).  Which workgroup computes a tile never changes its result.
+// E <= 64 (one lane per group); past that, index order.
+__device__ __forceinline__ int wgrad_slot_group(const WgradParams& p, int y) {
+  if (p.E > kWave || p.E == 1) return y;
+  const int lane = threadIdx.x & (kWave - 1);
+  int n = -1;
+  if (lane < p.E) {
+    int lo = lane > 0 ? p.offs[lane - 1] : 0;
+    int hi = p.offs[lane];
+    if (lo < 0) lo = 0;
+    if (hi > p.M) hi = (int)p.M;
+    n = hi > lo ? (hi + STEP - 1) / STEP - lo / STEP : 0;
+  }
+  int rank = 0;
+  for (int g = 0; g < p.E; ++g) {
+    const int v = lane_value(n, g);
+    rank += (v > n || (v == n && g < lane)) ? 1 : 0;
+  }
+  return __ffsll((long long)__ballot(lane < p.E && rank == y)) - 1;
+}
+
+// PIECES = false: grid (tiles_n * tiles_k, E), workgroup (x, y) computes tile
+// g * tiles_n * tiles_k + x of group g = wgrad_slot_group(y) whole when below
+// wgrad_whole (epilogue EPI); true: workgroup u computes the piece
+// wgrad_unit assigns it.
 template <class C, bool PIECES, int EPI = kEpiAny>
 __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
@@ -1335,7 +1363,9 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   if constexpr (PIECES) {
     if (!wgrad_unit<C>(p, (int)blockIdx.x, lt, piece, S)) return;
   } else {
-    lt = (int)blockIdx.y * p.tiles_n * p.tiles_k + (int)blockIdx.x;
+    // (wgrad_whole is every tile or none except for E = 1 or E > 64, where
+    // slots map to groups in index order)
+    lt = wgrad_slot_group(p, (int)blockIdx.y) * p.tiles_n * p.tiles_k + (int)blockIdx.x;
     if (lt >= wgrad_whole<C>(p)) return;
   }
   const WgradTile tl = wgrad_tile<C>(p, lt);
