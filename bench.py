@@ -40,6 +40,7 @@ import math
 import os
 import platform
 import random
+import re
 import statistics
 import sys
 import time
@@ -128,7 +129,7 @@ def copy_calibration(dev, mib: int = 256, reps: int = 3):
 def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shapes: int) -> str:
     """HBM bytes per launch of each GEMM kernel from two rocprofv3 --pmc passes
     (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) over
-    ``bench.py --steps S --warmup W --no-cpu --copy-calibration``.
+    ``bench.py --steps S --warmup W --no-cpu --no-bf16 --no-extra --copy-calibration``.
 
     Each counter is scaled so that the calibration copy (256 MiB each way)
     reads 256 MiB; dispatches are matched to sweep shapes by launch order
@@ -156,7 +157,8 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
         scaled[counter] = [(n, v * factor * 1024.0) for _, n, v in rows
                            if ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n]
     f, w = scaled["FETCH_SIZE"], scaled["WRITE_SIZE"]
-    per = warmup + steps
+    # each call is timed twice (plain scales, then step-major), warmup + steps launches each
+    per = 2 * (warmup + steps)
     shapes = SHAPES[:n_shapes]
     want = []
     for (e, n, k) in shapes:
@@ -258,8 +260,8 @@ def call_spans(trace_csv: str):
             cur[1] = max(cur[1], t1)
             if whole:
                 cur[2] = n
-            elif ", true, 0>" in n and ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n):
-                cur[4] = n.replace(", true, 0>", ", false, 1>")
+            elif ", true, " in n and ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n):
+                cur[4] = re.sub(r", true, \d+>$", ", false, 1>", n)
         else:
             close()
             cur = None

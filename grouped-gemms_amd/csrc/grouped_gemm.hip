@@ -896,11 +896,21 @@ struct FwdParams {
 // Epilogue of the whole-tile kernels, fixed at compile time so that the
 // common case carries none of the others' register pressure (with every
 // variant in one kernel the allocator spilled accumulators to scratch and
-// reloaded them serially in the epilogue): kEpiBf16 is a bf16 output whose
-// rows are 16-byte aligned (row stride a multiple of 8 elements, 16-byte
-// aligned base), staged through LDS; kEpiAny takes every output type and
-// alignment.
-constexpr int kEpiAny = 0, kEpiBf16 = 1;
+// reloaded them serially in the epilogue): kEpiBf16 / kEpiF16 are bf16 / f16
+// outputs whose rows are 16-byte aligned (row stride a multiple of 8
+// elements, 16-byte aligned base), staged through LDS; kEpiF32 stores f32
+// directly, and kEpiBf16Any / kEpiF16Any 16-bit rows off the 16-byte grid;
+// kEpiAny (the wgrad's other outputs) picks the type per call.
+constexpr int kEpiAny = 0, kEpiBf16 = 1, kEpiF16 = 2, kEpiF32 = 3, kEpiBf16Any = 4, kEpiF16Any = 5;
+
+// Epilogue of a whole-tile launch for this output (host side).
+inline int pick_epi(int out_dtype, int64_t ldo, const void* out) {
+  const bool al16 = ldo % 8 == 0 && (uintptr_t)out % 16 == 0;
+  if (al16 && out_dtype == MXGG_DTYPE_BF16) return kEpiBf16;
+  if (al16 && out_dtype == MXGG_DTYPE_F16) return kEpiF16;
+  if (out_dtype == MXGG_DTYPE_F32) return kEpiF32;
+  return out_dtype == MXGG_DTYPE_BF16 ? kEpiBf16Any : kEpiF16Any;
+}
 
 struct FwdTile {
   int expert;
@@ -984,14 +994,14 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
     ring_mainloop<C>(smem, X, W, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
     if constexpr (EPI == kEpiBf16) {
       store_tile_lds<C, true>(acc, smem, p.out + (row0 * p.ldo + n0) * 2, p.ldo, rows, cols);
+    } else if constexpr (EPI == kEpiF16) {
+      store_tile_lds<C, false>(acc, smem, p.out + (row0 * p.ldo + n0) * 2, p.ldo, rows, cols);
+    } else if constexpr (EPI == kEpiF32) {
+      store_tile<C, false>(acc, p.out + (row0 * p.ldo + n0) * 4, p.ldo, rows, cols, MXGG_DTYPE_F32);
     } else {
-      const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-      uint8_t* o = p.out + (row0 * p.ldo + n0) * esz;
-      if (esz == 2 && p.ldo % 8 == 0 && (uintptr_t)o % 16 == 0)
-        p.out_dtype == MXGG_DTYPE_BF16 ? store_tile_lds<C, true>(acc, smem, o, p.ldo, rows, cols)
-                                       : store_tile_lds<C, false>(acc, smem, o, p.ldo, rows, cols);
-      else
-        store_tile<C, false>(acc, o, p.ldo, rows, cols, p.out_dtype);
+      static_assert(EPI == kEpiBf16Any || EPI == kEpiF16Any, "forward epilogue");
+      store_tile<C, false>(acc, p.out + (row0 * p.ldo + n0) * 2, p.ldo, rows, cols,
+                           EPI == kEpiBf16Any ? MXGG_DTYPE_BF16 : MXGG_DTYPE_F16);
     }
   }
 }
@@ -1021,7 +1031,7 @@ __device__ __forceinline__ int fwd_groups(const FwdParams& p, WaveGroups& wg) {
 // into partial slot u.  Other workgroups exit.  (Two kernels rather than one
 // with both paths: sharing a register allocation slows the whole-tile loop by
 // ~2%.)
-template <class C, bool PIECES, int EPI = kEpiAny>
+template <class C, bool PIECES, int EPI = kEpiBf16>
 __global__ __launch_bounds__(C::NT) void fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[C::LDS];
   WaveGroups wg;
@@ -1410,13 +1420,9 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   }
   if constexpr (EPI == kEpiBf16) {
     store_tile_lds<C, true>(acc, smem, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * 2, p.K, rows, cols);
-  } else {
+  } else {   // f32, or bf16 rows off the 16-byte grid
     const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-    uint8_t* o = p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz;
-    if (esz == 2 && p.K % 8 == 0 && (uintptr_t)o % 16 == 0)
-      store_tile_lds<C, true>(acc, smem, o, p.K, rows, cols);   // wgrad: bf16 or f32 only
-    else
-      store_tile<C, true>(acc, o, p.K, rows, cols, p.out_dtype);
+    store_tile<C, true>(acc, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz, p.K, rows, cols, p.out_dtype);
   }
 }
 
@@ -1502,7 +1508,10 @@ namespace {
 
 typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_256;
 typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_128;
-typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 5> CfgF4_256;
+// e2m1 weights: stages of 24 KB in a 4-deep ring, like e4m3 (a 5-deep ring
+// measured the same on BASELINE config 5, 650 vs 651 us, and spilled 8 bytes
+// per lane in the LDS-staged epilogues)
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 4> CfgF4_256;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -1619,20 +1628,32 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   const int64_t tiles_ub = (int64_t)grid_m_ub * p.grid_n;
   if (tiles_ub <= 0) return MXGG_OK;
   if (tiles_ub > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
-  const bool bf16 = p.out_dtype == MXGG_DTYPE_BF16 && p.ldo % 8 == 0 && (uintptr_t)p.out % 16 == 0;
-  if (bf16)
-    hipLaunchKernelGGL((fwd_kernel<C, false, kEpiBf16>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
-  else
-    hipLaunchKernelGGL((fwd_kernel<C, false, kEpiAny>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p);
+  const int epi = pick_epi(p.out_dtype, p.ldo, p.out);
+  switch (epi) {
+#define MXGG_WHOLE(E) \
+  case E: hipLaunchKernelGGL((fwd_kernel<C, false, E>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p); break
+    MXGG_WHOLE(kEpiBf16);
+    MXGG_WHOLE(kEpiF16);
+    MXGG_WHOLE(kEpiF32);
+    MXGG_WHOLE(kEpiBf16Any);
+    MXGG_WHOLE(kEpiF16Any);
+#undef MXGG_WHOLE
+  }
   if (int rc = launch_status("grouped_mm")) return rc;
   if constexpr (std::is_same<C, CfgF8_256>::value) {
     if (p.quads) {   // 4 * (T % P) <= P quarters
-      if (bf16)
-        hipLaunchKernelGGL((fwd_quad_kernel<C, CfgF8_128, kEpiBf16>), dim3((unsigned)p.par), dim3(CfgF8_128::NT),
-                           0, st, p);
-      else
-        hipLaunchKernelGGL((fwd_quad_kernel<C, CfgF8_128, kEpiAny>), dim3((unsigned)p.par), dim3(CfgF8_128::NT),
-                           0, st, p);
+      switch (epi) {
+#define MXGG_QUAD(E)                                                                                         \
+  case E:                                                                                                   \
+    hipLaunchKernelGGL((fwd_quad_kernel<C, CfgF8_128, E>), dim3((unsigned)p.par), dim3(CfgF8_128::NT), 0, st, p); \
+    break
+        MXGG_QUAD(kEpiBf16);
+        MXGG_QUAD(kEpiF16);
+        MXGG_QUAD(kEpiF32);
+        MXGG_QUAD(kEpiBf16Any);
+        MXGG_QUAD(kEpiF16Any);
+#undef MXGG_QUAD
+      }
       if (int rc = launch_status("grouped_mm")) return rc;
     }
   }
