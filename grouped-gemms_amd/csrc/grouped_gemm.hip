@@ -2007,8 +2007,10 @@ extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t
   if (E <= 0 || M < 0 || N < 0 || K < 0) return 0;
   const size_t sc = wgrad_scale_bytes(M, N, K);
   if (sc == 0 || N == 0 || K == 0) return sc;
+  // With several groups the kernels plan a lone under-filled round from the
+  // longest group, which may hold all M tokens: room for that plan.
   const size_t part = split_area((int64_t)E * cdiv(N, 256) * cdiv(K, 256), (size_t)256 * 256 * 4,
-                                 wgrad_group_steps(E, M));
+                                 E > 1 ? cdiv(M, STEP) : wgrad_group_steps(E, M));
   return part ? align256(sc) + part : sc;
 }
 

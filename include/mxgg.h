@@ -260,7 +260,8 @@ int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
  *         recommended: mxgg_wgrad_workspace_size(E, M, N, K), which adds room
  *         for the fp32 partial tiles of tiles cut along the token range when
  *         the tiles do not fill the chip (E = 1, or fewer tiles than
- *         resident workgroups).
+ *         resident workgroups; with E > 1 sized for a group of all M tokens,
+ *         since the kernels cut by the longest group), at most 128 MiB.
  */
 size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,

@@ -114,8 +114,11 @@ def test_grouped_mm_workspace_without_gpu():
     assert lib.mxgg_grouped_mm_workspace_size(1, 256, 256, 4096) == 4 * 32 * (256 + 256) + 2 * MiB
     # wgrad E=4, M=16640: 33 steps per average group -> 8 pieces; 640 tiles -> cap
     assert lib.mxgg_wgrad_workspace_size(4, 16640, 2048, 5120) == 4 * 130 * (2048 + 5120) + 128 * MiB
-    # wgrad E=8, M=16640: 17 steps per average group -> no split
-    assert lib.mxgg_wgrad_workspace_size(8, 16640, 256, 256) == 4 * 130 * (256 + 256)
+    # wgrad E=8, N=K=256: 8 tiles; with several groups the room is sized for one
+    # group holding all 130 steps -> 8 pieces of each tile (8 x 8 x 256 KiB)
+    assert lib.mxgg_wgrad_workspace_size(8, 16640, 256, 256) == 4 * 130 * (256 + 256) + 16 * MiB
+    # wgrad E=1, M=2048: 16 steps -> no split
+    assert lib.mxgg_wgrad_workspace_size(1, 2048, 256, 256) == 4 * 16 * (256 + 256)
     rc = lib.mxgg_grouped_mm(16, 64, 16, 2, 16, 0, 64, 64 * 64, 16, 2, 128, 16, 1, 64, 64, 64,
                              16, 0, 64, 0, 0, 0, 0, None, 0, None)
     assert rc == _lib.ERR_WORKSPACE and b"workspace" in lib.mxgg_last_error_string()

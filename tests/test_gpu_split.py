@@ -213,12 +213,25 @@ def _wgrad_abi(qg, sg, qi, si, offs_t, out_dtype, ws_bytes):
     return out
 
 
+def _many_groups():
+    """80 groups (a fifth empty, sizes off the 32 grid) with one long group:
+    E > 64 takes the device plan's single piece count, set by the longest
+    group, for a lone under-filled round of 80 tiles."""
+    rng = np.random.default_rng(2080)
+    sizes = rng.integers(0, 600, 80)
+    sizes[rng.choice(80, 16, replace=False)] = 0
+    sizes[37] = 20000
+    offs = np.cumsum(sizes)
+    return [int(v) for v in offs], int(offs[-1] + 31) // 32 * 32 + 64
+
+
 @pytest.mark.parametrize("E,M,N,K,offs,out_dtype", [
     (1, 8192, 512, 512, [8192], torch.bfloat16),               # 4 tiles, 64 steps -> 8 pieces
     (3, 24576, 320, 288, [0, 8000, 24576], torch.bfloat16),    # empty group, bounds not at 128
     (2, 16384, 256, 512, [8160, 16384], torch.float32),        # f32 out (bf16-rounded values)
     (2, 16384, 512, 512, [1024, 16384], torch.bfloat16),       # 8 vs 120 steps: per-group piece counts
     (1, 16640, 2560, 3584, [16640], torch.bfloat16),           # 140 tiles > P / 2: pieces in two rounds
+    (80, _many_groups()[1], 256, 256, _many_groups()[0], torch.bfloat16),   # E > 64: one piece count
 ])
 def test_wgrad_split_matches_whole_tiles(gpu, E, M, N, K, offs, out_dtype):
     import kernels
