@@ -82,10 +82,21 @@ __device__ __forceinline__ uint32_t gather4(uint32_t s, int j) {
   return v;
 }
 
+// 16 source bytes, read once: a non-temporal load, which leaves the lines
+// already in L2 / the memory-side cache (often the producer's dirty output)
+// in place instead of evicting them.  Streaming 16640 x 8192 bf16 after a
+// 512 MB cache-dirtying fill: 98 us instead of 121 us for a copy-shaped
+// kernel; with clean caches both take 82 us.
+__device__ __forceinline__ uint4 load16_stream(const uint8_t* p) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 template <int SRC>
 __device__ __forceinline__ void load8(const uint8_t* p, float (&v)[8]) {
   if constexpr (SRC == MXGG_DTYPE_BF16) {
-    uint4 u = *reinterpret_cast<const uint4*>(p);
+    uint4 u = load16_stream(p);
     uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -93,13 +104,13 @@ __device__ __forceinline__ void load8(const uint8_t* p, float (&v)[8]) {
       v[2 * i + 1] = bf16_to_f32(w[i] >> 16);
     }
   } else if constexpr (SRC == MXGG_DTYPE_F16) {
-    uint4 u = *reinterpret_cast<const uint4*>(p);
+    uint4 u = load16_stream(p);
     const _Float16* h = reinterpret_cast<const _Float16*>(&u);
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = (float)h[i];
   } else {
-    uint4 u0 = *reinterpret_cast<const uint4*>(p);
-    uint4 u1 = *reinterpret_cast<const uint4*>(p + 16);
+    uint4 u0 = load16_stream(p);
+    uint4 u1 = load16_stream(p + 16);
     v[0] = __uint_as_float(u0.x); v[1] = __uint_as_float(u0.y);
     v[2] = __uint_as_float(u0.z); v[3] = __uint_as_float(u0.w);
     v[4] = __uint_as_float(u1.x); v[5] = __uint_as_float(u1.y);
@@ -289,7 +300,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MXGG_QTILE_
     for (int i = 0; i < NCH; ++i) {
       const int idx = t + 256 * i;
       const int rr = idx / CPR, c = (idx % CPR) * EPC;
-      u[i] = (rr < tr && c < tc) ? *reinterpret_cast<const uint4*>(src + (r0 + rr) * ld_src_bytes + (c0 + c) * EB)
+      u[i] = (rr < tr && c < tc) ? load16_stream(src + (r0 + rr) * ld_src_bytes + (c0 + c) * EB)
                                  : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
