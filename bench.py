@@ -25,7 +25,8 @@ kernels read, so the call launches no re-layout): between its events lie
 only the GEMM launches of the call (the whole-tile kernel, and the piece /
 quarter-tile / reduce launches when its last round is split).  The roofline
 of the dominant kernel uses that time.  Also measured
-(e4m3 x e2m1, E=8, M=16640, N=8192, K=5120) and the quantizer in GB/s.
+(e4m3 x e2m1, E=8, M=16640, N=8192, K=5120), the quantizer in GB/s and one
+training step (forward + backward) of the MoE layer (kernels/moe.py).
 
 Prints ONE JSON line on stdout; progress and the per-shape table go to stderr
 and to gpurun_out/bench_detail.json when that directory exists.
@@ -400,8 +401,62 @@ def extra_measurements(dev, args, flush):
                        "frac_of_copy_rate": round(gbs / copy_gbs, 4)}
     del x
     torch.cuda.empty_cache()
-    log(json.dumps({"cfg5": cfg5, "quant": quant}))
-    return {"cfg5": cfg5, "quant": quant}
+    moe = moe_layer_measurement(dev, args, flush)
+    log(json.dumps({"cfg5": cfg5, "quant": quant, "moe_layer": moe}))
+    return {"cfg5": cfg5, "quant": quant, "moe_layer": moe}
+
+
+def moe_layer_measurement(dev, args, flush):
+    """One training step of the MoE expert projection (kernels/moe.py):
+    forward and backward of MXFP8GroupedLinear(E=8, 5120 -> 8192) on 16640
+    tokens (offsets random.seed(5)), i.e. to_mx_both of x, w and grad_out, the
+    forward GEMM, dgrad and wgrad; 6*M*N*K FLOPs per step.  Beside it, the
+    three GEMMs alone on the same step-major operands, so the rest of the step
+    (quantization, allocation, autograd) is step - GEMMs."""
+    import torch
+    from kernels import to_mx_both, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
+    from kernels.moe import MXFP8GroupedLinear
+    from utils import generate_jagged_offs
+    M, E, K, N = M_TOKENS, 8, 5120, 8192
+    random.seed(5)
+    offs = generate_jagged_offs(E, M, multiple_of=32, device=dev)
+    torch.manual_seed(5)
+    layer = MXFP8GroupedLinear(E, K, N, device=dev)
+    x = torch.randn((M, K), device=dev).to(torch.bfloat16).requires_grad_()
+    g = torch.randn((M, N), device=dev).to(torch.bfloat16)
+
+    def fwd():
+        with torch.no_grad():
+            layer(x, offs)
+
+    def step():
+        x.grad = None
+        layer.weight.grad = None
+        layer(x, offs).backward(g)
+
+    fmed, _ = time_call(fwd, args.steps, args.warmup, flush)
+    smed, _ = time_call(step, args.steps, args.warmup, flush)
+    x.grad = None
+    layer.weight.grad = None
+    with torch.no_grad():
+        (sx, qx), (sxt, qxt) = to_mx_both(x.detach(), scale_layout="steps")
+        (sw, qw), (swt, qwt) = to_mx_both(layer.weight.detach(), scale_layout="steps")
+        (sg, qg), (sgt, qgt) = to_mx_both(g, scale_layout="steps")
+    gemm = {
+        "fwd": time_call(lambda: triton_mxfp8_grouped_mm(qx, qw, sx, sw, offs), args.steps, args.warmup, flush)[0],
+        "dgrad": time_call(lambda: triton_mxfp8_grouped_mm(qg, qwt, sg, swt, offs), args.steps, args.warmup,
+                           flush)[0],
+        "wgrad": time_call(lambda: triton_mxfp8_wgrad(qgt, sgt, qxt, sxt, offs), args.steps, args.warmup, flush)[0],
+    }
+    del layer, x, g, qx, qw, qxt, qwt, qg, qgt, sx, sw, sxt, swt, sg, sgt
+    torch.cuda.empty_cache()
+    gsum = sum(gemm.values())
+    return {"workload": "MXFP8GroupedLinear E=8, 5120 -> 8192, M=16640 bf16 tokens, offs random.seed(5): "
+                        "forward + backward (to_mx_both of x, w, grad_out; fwd, dgrad, wgrad GEMMs)",
+            "fwd_us": round(fmed * 1e3, 1), "step_us": round(smed * 1e3, 1),
+            "step_tflops": round(6.0 * M * N * K / (smed * 1e-3) / 1e12, 1),
+            "gemm_only_us": {k: round(v * 1e3, 1) for k, v in gemm.items()},
+            "gemm_share_of_step": round(gsum / smed, 4)}
 
 
 def main():
@@ -617,6 +672,7 @@ def main():
                                        for d in ("fwd", "dgrad", "wgrad")},
         "cfg5_mxfp4": extra["cfg5"] if extra else None,
         "quantizer": extra["quant"] if extra else None,
+        "moe_layer": extra["moe_layer"] if extra else None,
         "fwd_geomean_by_E": per_e,
         "baseline_note": "vs_baseline = fwd geomean / 1498.8 TFLOP/s (reference README table, MI355X)",
         "roofline": roofline,
