@@ -287,14 +287,22 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
     for text in open(bench_json):
         if text.startswith("{"):
             line = json.loads(text)
+    bench_calls = {}
+    if line and line.get("roofline"):
+        bench_calls = {canon(k): v["launches"] for k, v in line["roofline"]["by_kernel"].items()}
     if trace_csv:
         out += ["", "Per call, from the kernel trace: the span of each call's GEMM dispatches (whole-tile kernel "
-                    "and any split / quarter-tile / reduce launches), by the call's whole-tile kernel:"]
+                    "and any split / quarter-tile / reduce launches), by the call's whole-tile kernel; the sweep's "
+                    "timed kernel-only calls are the first cold ones, since the sweep runs first:"]
         for name, v in sorted(call_spans(trace_csv).items()):
             cold = [t for t, c in v if c]
-            out.append(f"  {name:62s} all calls {len(v):6d}: avg {sum(t for t, _ in v) / len(v) / 1e3:9.2f} us;  "
-                       f"right after the cache flush {len(cold):6d}: avg "
-                       f"{(sum(cold) / len(cold) / 1e3) if cold else float('nan'):9.2f} us")
+            text = (f"  {name:62s} all calls {len(v):6d}: avg {sum(t for t, _ in v) / len(v) / 1e3:9.2f} us;  "
+                    f"right after the cache flush {len(cold):6d}: avg "
+                    f"{(sum(cold) / len(cold) / 1e3) if cold else float('nan'):9.2f} us")
+            nb = bench_calls.get(canon(name))
+            if nb and len(cold) >= nb:
+                text += f";  the sweep's first {nb}: avg {sum(cold[:nb]) / nb / 1e3:9.2f} us"
+            out.append(text)
     if line and line.get("roofline"):
         rf = line["roofline"]
         out += ["", "Same run, bench.py's own figures (HIP events on the launch stream, timed reps only):"]
