@@ -169,30 +169,30 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
             else:
                 nn, kk = (n, k) if kind == "fwd" else (k, n)
                 alg = M_TOKENS * kk * (1 + 1 / 32) + e * nn * kk * (1 + 1 / 32) + 2 * M_TOKENS * nn
-            want += [(kind, alg)] * per
+            want += [(kind, alg, (e, n, k))] * per
     if len(f) != len(w):
         raise SystemExit(f"dispatch count mismatch: fetch {len(f)}, write {len(w)}")
     # a wgrad call whose tiles are all split launches no whole-tile kernel:
     # its entry in `want` has no dispatch and is skipped
     matched = []
     i = 0
-    for kind, alg in want:
+    for kind, alg, shape in want:
         if i < len(f) and (("wgrad" in f[i][0]) == (kind == "wgrad")):
-            matched.append((f[i], w[i], (kind, alg)))
+            matched.append((f[i], w[i], (kind, alg, shape)))
             i += 1
         elif kind != "wgrad":
             raise SystemExit(f"dispatch {i} ({f[i][0] if i < len(f) else 'none'}) does not match a {kind} call")
     if i != len(f):
         raise SystemExit(f"{len(f) - i} dispatches left unmatched")
-    agg = {}
-    for (nf, vf), (nw, vw), (kind, alg) in matched:
+    agg, by_shape = {}, {}
+    for (nf, vf), (nw, vw), (kind, alg, shape) in matched:
         assert nf == nw and (("wgrad" in nf) == (kind == "wgrad")), (nf, nw, kind)
         name = nf.replace("void ", "").split("(")[0]
-        a = agg.setdefault(name, [0.0, 0.0, 0.0, 0])
-        a[0] += vf
-        a[1] += vw
-        a[2] += alg
-        a[3] += 1
+        for a in (agg.setdefault(name, [0.0, 0.0, 0.0, 0]), by_shape.setdefault((shape, kind), [0.0, 0.0, 0.0, 0])):
+            a[0] += vf
+            a[1] += vw
+            a[2] += alg
+            a[3] += 1
     out.append(f"{'kernel':58s} {'launches':>8s} {'fetch MB':>9s} {'write MB':>9s} {'total MB':>9s} "
                f"{'algorithmic MB':>14s} {'ratio':>6s}")
     for name, (vf, vw, alg, c) in sorted(agg.items()):
@@ -200,6 +200,10 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
                    f"{alg / c / 1e6:14.1f} {(vf + vw) / alg:6.2f}")
     for name, (vf, vw, alg, c) in sorted(agg.items()):
         out.append(f"traffic_bytes_per_launch {name} = {(vf + vw) / c:.0f}")
+    out += ["", "Per shape (E, N, K) and direction, whole-tile kernel: fetch + write MB per launch / algorithmic MB"]
+    for (shape, kind), (vf, vw, alg, c) in sorted(by_shape.items()):
+        out.append(f"  {shape[0]} {shape[1]:5d} {shape[2]:5d} {kind:5s} {vf / c / 1e6:8.1f} + {vw / c / 1e6:6.1f}"
+                   f" / {alg / c / 1e6:6.1f} = {(vf + vw) / alg:5.2f}")
     return "\n".join(out)
 
 
