@@ -183,16 +183,6 @@ __device__ __forceinline__ uint32_t quant32(const float (&v)[32], uint8_t* dst) 
   return sc;
 }
 
-// Launch shape knobs (experiments override them with -D): the row kernel's
-// grid cap (0: one pass, a workgroup per 64 blocks) and a waves-per-SIMD hint
-// for the tile kernel (1: none).
-#ifndef MXGG_QROWS_CAP
-#define MXGG_QROWS_CAP 0
-#endif
-#ifndef MXGG_QTILE_WPE
-#define MXGG_QTILE_WPE 1
-#endif
-
 // Row-wise quantization: four lanes (a quad) own one 32-element block, 8
 // elements each; a workgroup's 64 quads take 64 consecutive blocks (a
 // contiguous 4 KB of bf16), one grid-stride pass per 64 * gridDim.x blocks.
@@ -273,7 +263,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restri
 // lanes of a group, reading four bands of one column, hit disjoint banks.
 // rows % 32 == 0: a partial last tile has whole 32-row blocks.
 template <int SRC, bool ROWS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MXGG_QTILE_WPE))) void quant_tile_kernel(
+__global__ __launch_bounds__(256) void quant_tile_kernel(
     const uint8_t* __restrict__ src, int64_t rows, int64_t cols, int64_t ld_src_bytes, uint8_t* __restrict__ q_r,
     int64_t ld_qr, ScaleOut s_r, uint8_t* __restrict__ q_c, int64_t ld_qc, ScaleOut s_c) {
   constexpr int EB = elem_bytes<SRC>();
@@ -406,10 +396,10 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: output rows misaligned");
   if (int rc = require_device()) return rc;
   const int64_t nblk = rows * (cols / 32);
-  // 64 quads per 256-thread workgroup, one block each: one pass
+  // 64 quads per 256-thread workgroup, one block each: one pass (the kernel
+  // strides over the grid, so a capped grid only takes more passes)
   const int64_t want = (nblk + 63) / 64;
-  const int64_t cap = MXGG_QROWS_CAP > 0 ? MXGG_QROWS_CAP : INT32_MAX;
-  const int grid = (int)(want < cap ? (want < 1 ? 1 : want) : cap);
+  const int grid = (int)(want < 1 ? 1 : (want < INT32_MAX ? want : INT32_MAX));
   hipStream_t st = (hipStream_t)stream;
   const uint8_t* s8 = (const uint8_t*)src;
   uint8_t* q8 = (uint8_t*)q;
