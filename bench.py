@@ -25,8 +25,9 @@ kernels read, so the call launches no re-layout): between its events lie
 only the GEMM launches of the call (the whole-tile kernel, and the piece /
 quarter-tile / reduce launches when its last round is split).  The roofline
 of the dominant kernel uses that time.  Also measured
-(e4m3 x e2m1, E=8, M=16640, N=8192, K=5120), the quantizer in GB/s and one
-training step (forward + backward) of the MoE layer (kernels/moe.py).
+(e4m3 x e2m1, E=8, M=16640, N=8192, K=5120), the quantizer in GB/s, one
+training step (forward + backward) of the MoE layer (kernels/moe.py) and one
+GPU's share of the sweep under 8-way expert parallelism (E=1, M=2080).
 
 Prints ONE JSON line on stdout; progress and the per-shape table go to stderr
 and to gpurun_out/bench_detail.json when that directory exists.
@@ -414,8 +415,43 @@ def extra_measurements(dev, args, flush):
     del x
     torch.cuda.empty_cache()
     moe = moe_layer_measurement(dev, args, flush)
-    log(json.dumps({"cfg5": cfg5, "quant": quant, "moe_layer": moe}))
-    return {"cfg5": cfg5, "quant": quant, "moe_layer": moe}
+    ep = ep_shard_measurement(dev, args, flush)
+    log(json.dumps({"cfg5": cfg5, "quant": quant, "moe_layer": moe, "ep_shard": ep}))
+    return {"cfg5": cfg5, "quant": quant, "moe_layer": moe, "ep_shard": ep}
+
+
+def ep_shard_measurement(dev, args, flush):
+    """One GPU's share of the sweep under 8-way expert parallelism: E=8 over
+    8 GPUs leaves one expert and about M/8 = 2080 tokens per GPU, so each
+    (N, K) of the sweep becomes an E=1, M=2080 problem (a few hundred tiles,
+    where the last round's handling decides the time).  Forward and wgrad,
+    drop-in calls, geomean TFLOP/s over the 9 (N, K)."""
+    import torch
+    from kernels import to_mx, to_mx_dim0, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
+    M = M_TOKENS // 8
+    offs = torch.tensor([M], dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(8)
+    rows = []
+    for n, k in itertools.product((2048, 5120, 8192), (2048, 5120, 8192)):
+        a = torch.randn((M, k), device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.randn((1, n, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        go = torch.randn((M, n), device=dev, generator=g).to(torch.bfloat16)
+        sa, qa = to_mx(a)
+        sw, qw = to_mx(w)
+        sg, qg = to_mx_dim0(go)
+        si, qi = to_mx_dim0(a)
+        flops = 2.0 * M * n * k
+        fmed, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs), args.steps, args.warmup, flush)
+        wmed, _ = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs), args.steps, args.warmup, flush)
+        rows.append({"N": n, "K": k, "fwd_us": round(fmed * 1e3, 1), "fwd_tflops": round(flops / (fmed * 1e-3) / 1e12, 1),
+                     "wgrad_us": round(wmed * 1e3, 1), "wgrad_tflops": round(flops / (wmed * 1e-3) / 1e12, 1)})
+        del a, w, go, sa, qa, sw, qw, sg, qg, si, qi
+    torch.cuda.empty_cache()
+    return {"workload": "E=1, M=2080 (16640 tokens / 8 GPUs), N, K in (2048, 5120, 8192): one GPU's expert-parallel "
+                        "share of the sweep's E=8 shapes, drop-in calls",
+            "fwd_geomean_tflops": round(geomean([r["fwd_tflops"] for r in rows]), 1),
+            "wgrad_geomean_tflops": round(geomean([r["wgrad_tflops"] for r in rows]), 1),
+            "rows": rows}
 
 
 def moe_layer_measurement(dev, args, flush):
@@ -685,6 +721,7 @@ def main():
         "cfg5_mxfp4": extra["cfg5"] if extra else None,
         "quantizer": extra["quant"] if extra else None,
         "moe_layer": extra["moe_layer"] if extra else None,
+        "ep_shard": extra["ep_shard"] if extra else None,
         "fwd_geomean_by_E": per_e,
         "baseline_note": "vs_baseline = fwd geomean / 1498.8 TFLOP/s (reference README table, MI355X)",
         "roofline": roofline,

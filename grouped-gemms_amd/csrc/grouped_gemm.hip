@@ -1542,19 +1542,32 @@ const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
 // tiles, the 8-XCD swizzle and expert-aligned bands of at most 12 m-blocks
 // (route_tile; 12 beat 8 and 16 on the sweep's jagged groups, and the
 // 256 x 256 tile beats 128 x 128 even at N = K = 2048); 128 x 128 tiles for
-// e4m3 problems too small to fill half the chip with 256 x 256 tiles and too
-// short (K < 4096) for the split of the last round to make up for it.
+// e4m3 problems too small to fill half the chip with 256 x 256 tiles, unless
+// the 256 x 256 plan splits that lone round along K.
 // Requests (nonzero bm, bn, gm, xcd) override field by field, and any request
 // leaves the split to the workspace (a tuned "whole tiles only" applies to
 // calls that request nothing).
+template <class C>
+int fwd_resident();
+
 FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, int bn, int gm,
                    int xcd) {
   FwdChoice c{256, 256, 12, 8, true};
+  const int64_t tiles256 = (cdiv(M, 256) + E - 1) * cdiv(N, 256);
   if (const TunedFwd* t = find_tuned(E, M, N, K, b_fmt)) {
     c = FwdChoice{t->bm, t->bn, t->group_m, t->xcd, t->split != 0};
-  } else if (b_fmt == MXGG_FMT_E4M3 && K < 4096 && (cdiv(M, 256) + E - 1) * cdiv(N, 256) < 128) {
-    c.bm = 128;
-    c.bn = 128;
+  } else if (b_fmt == MXGG_FMT_E4M3 && tiles256 < 128) {
+    // Under half a chip of 256 x 256 tiles: 128 x 128 tiles (two per CU)
+    // spread the work over 4x the workgroups, unless the 256 x 256 launch
+    // splits its lone round along K (a long reduction).  E=1, M=2080 (one
+    // GPU's share of E=8 under 8-way expert parallelism), N=2048: K=5120
+    // 77 -> 54 us; K=8192 splits (70 us, against 76 us as 128 x 128).
+    const int par = fwd_resident<CfgF8_256>();
+    const int slots = (int)(kSplitBytes / ((size_t)256 * 256 * 4));
+    if (split_plan((int)tiles256, par > 0 ? par : 256, (int)cdiv(K, STEP), slots, 256).units == 0) {
+      c.bm = 128;
+      c.bn = 128;
+    }
   }
   if (bm || bn || gm || xcd) c.split = true;
   if (bm) c.bm = bm;
@@ -1664,10 +1677,17 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   const int pieces = p.slots;   // units = rem * S <= slots
   hipLaunchKernelGGL((fwd_kernel<C, true>), dim3((unsigned)pieces), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("grouped_mm")) return rc;
-  // a split needs rem <= par / 2 tiles of ReduceShape::CH items each; a small
-  // grid loops over them (and costs little when the plan has no split)
+  // a split needs rem <= par / 2 tiles of ReduceShape::CH items each; the
+  // grid strides over them.  One workgroup per item of the split the host
+  // expects (at least 128, which costs little when the device plan differs):
+  // a 72-tile split (1152 items) took 21 us on 128 workgroups.
   const int64_t items = (int64_t)(p.par / 2) * ReduceShape<C>::CH;
-  const int64_t rgrid = items < 128 ? items : 128;
+  const int64_t est = (cdiv(p.M, C::BM) + (p.E - 1) / 2) * p.grid_n;
+  const Split esp = split_plan((int)(est < INT32_MAX ? est : INT32_MAX), p.par, nsteps, p.slots,
+                               C::BM * C::BN * 4 / 1024);
+  int64_t rgrid = esp.S > 0 ? (int64_t)(esp.units / esp.S) * ReduceShape<C>::CH : 0;
+  if (rgrid < 128) rgrid = 128;
+  if (rgrid > items) rgrid = items;
   if (rgrid <= 0) return MXGG_OK;
   hipLaunchKernelGGL((fwd_reduce_kernel<C>), dim3((unsigned)rgrid), dim3(256), 0, st, p);
   return launch_status("grouped_mm");
