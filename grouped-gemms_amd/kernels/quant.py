@@ -45,14 +45,14 @@ def _layout_code(scale_layout: str) -> int:
     raise ValueError(f"scale_layout must be 'plain' or 'steps', got {scale_layout!r}")
 
 
-def _token_rows(batch: tuple, rows: int, length: int, device) -> tuple:
-    """Output ``(*batch, rows, length)`` uint8 whose rows start 128 bytes
-    apart at least: a view of a buffer with the row stride rounded up to a
-    multiple of 128 when ``length`` is not one (the transposed, token-major
-    operands of the weight gradient, whose length is the token count).  The
-    GEMM copies operand rows in 64-byte pieces; rows off the 128-byte grid
-    put a quarter of them across two cache lines (wgrad at 2080 tokens:
-    12-16% slower).  Returns ``(view, row stride)``."""
+def _aligned_rows(batch: tuple, rows: int, length: int, device) -> tuple:
+    """Output ``(*batch, rows, length)`` uint8 whose rows start on the
+    128-byte grid: a view of a buffer with the row stride rounded up to a
+    multiple of 128 when ``length`` is not one (e.g. the token-major operands
+    of the weight gradient, whose length is the token count).  The GEMM
+    copies operand rows in 64-byte pieces; rows off the 128-byte grid put a
+    quarter of them across two cache lines (wgrad at 2080 tokens: 12-16%
+    slower).  Returns ``(view, row stride)``."""
     ld = (length + 127) // 128 * 128
     buf = torch.empty(tuple(batch) + (rows, ld), dtype=torch.uint8, device=device)
     return buf[..., :length], ld
@@ -135,7 +135,7 @@ def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
     if (C * x.element_size()) % 16:
         raise ValueError(f"to_mx_dim0 needs dim 1 ({C}) to span a multiple of 16 bytes")
     lay = _layout_code(scale_layout)
-    q, ld_q = _token_rows((), C, R, data.device)
+    q, ld_q = _aligned_rows((), C, R, data.device)
     if lay == _lib.SCALES_STEPS:
         s = torch.empty(step_scales_shape((), C, R), dtype=torch.int32, device=data.device)
         ld_s = C
@@ -158,9 +158,9 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
     32.  Returns ``((scales (.., R, C//32), data (.., R, C)),
     (scales (.., C, R//32), data (.., C, R)))``, e4m3, bit-identical to the
     two separate calls.  ``scale_layout="steps"``: step-major int32 scales
-    ``(.., cdiv(C, 128), R)`` and ``(.., cdiv(R, 128), C)``.  When R is not a
-    multiple of 128 the transposed data is a view whose row stride is R
-    rounded up to 128 (as in ``to_mx_dim0``).
+    ``(.., cdiv(C, 128), R)`` and ``(.., cdiv(R, 128), C)``.  Either data
+    output whose row length (C, resp. R) is not a multiple of 128 is a view
+    with the row stride rounded up to 128 (as in ``to_mx_dim0``).
     """
     assert elem_dtype is torch.float8_e4m3fn, "to_mx_both supports e4m3fn only"
     assert block_size == 32, "block_size must be 32 (OCP MX)"
@@ -176,8 +176,8 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
         raise ValueError(f"to_mx_both needs the last dim ({C}) to span a multiple of 16 bytes")
     dev = data.device
     lay = _layout_code(scale_layout)
-    q_r = torch.empty((B, R, C), dtype=torch.uint8, device=dev)
-    q_c, ld_qc = _token_rows((B,), C, R, dev)
+    q_r, ld_qr = _aligned_rows((B,), R, C, dev)
+    q_c, ld_qc = _aligned_rows((B,), C, R, dev)
     if lay == _lib.SCALES_STEPS:
         s_r = torch.empty(step_scales_shape((B,), R, C), dtype=torch.int32, device=dev)
         s_c = torch.empty(step_scales_shape((B,), C, R), dtype=torch.int32, device=dev)
@@ -187,7 +187,7 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
         s_c = torch.empty((B, C, R // 32), dtype=torch.uint8, device=dev)
         ld_r, ld_c = C // 32, R // 32
     lib = _lib.load()
-    rc = lib.mxgg_quantize_mx_both(x.data_ptr(), code, B, R, C, C, q_r.data_ptr(), C, s_r.data_ptr(), ld_r,
+    rc = lib.mxgg_quantize_mx_both(x.data_ptr(), code, B, R, C, C, q_r.data_ptr(), ld_qr, s_r.data_ptr(), ld_r,
                                    q_c.data_ptr(), ld_qc, s_c.data_ptr(), ld_c, lay, _stream_handle(dev))
     _lib.check(rc)
     q_r, q_c = q_r.view(torch.float8_e4m3fn), q_c.view(torch.float8_e4m3fn)
