@@ -123,3 +123,31 @@ def test_quant_golden_cfg1(gpu):
     np.testing.assert_array_equal(bits_u8(qa), z["a_q"])
     np.testing.assert_array_equal(bits_u8(sb), z["b_scales"])
     np.testing.assert_array_equal(bits_u8(qb), z["b_q"])
+
+
+@pytest.mark.parametrize("shape", [(2080, 256), (96, 544), (4096, 160)])
+def test_quant_outputs_on_128_byte_rows(gpu, shape):
+    """to_mx_dim0 / to_mx_both return rows on the 128-byte grid (a strided
+    view when the row length is not a multiple of 128) holding exactly the
+    bytes of the contiguous results, and the weight-gradient GEMM gives the
+    same bits on them as on contiguous copies."""
+    import kernels
+    R, C = shape
+    x = randn_bf16((R, C), 1.0, R + C).to(gpu)
+    s_d, q_d = kernels.to_mx_dim0(x)
+    (s_r, q_r), (s_c, q_c) = kernels.to_mx_both(x)
+    for q, length in ((q_d, R), (q_c, R), (q_r, C)):
+        assert q.stride(-1) == 1 and q.stride(-2) % 128 == 0 and q.stride(-2) - length < 128
+        assert q.data_ptr() % 128 == 0
+    rs, rq = O.to_mx(bits_u16(x.cpu()), src="bf16")
+    cs, cq = O.to_mx(bits_u16(x.cpu().t().contiguous()), src="bf16")
+    np.testing.assert_array_equal(bits_u8(q_r), rq)
+    np.testing.assert_array_equal(bits_u8(q_c), cq)
+    np.testing.assert_array_equal(bits_u8(q_d), cq)
+    np.testing.assert_array_equal(bits_u8(s_c), cs)
+    # the GEMM reads the strided operands: same bits as on contiguous copies
+    offs = torch.tensor([R // 2 // 32 * 32, R], dtype=torch.int32, device=gpu)
+    w_strided = kernels.triton_mxfp8_wgrad(q_c, s_c, q_d, s_d, offs)
+    w_contig = kernels.triton_mxfp8_wgrad(q_c.contiguous(), s_c, q_d.contiguous(), s_d, offs)
+    torch.cuda.synchronize()
+    assert torch.equal(w_strided.view(torch.int16), w_contig.view(torch.int16))
