@@ -1559,7 +1559,8 @@ FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, in
   } else if (b_fmt == MXGG_FMT_E4M3 && tiles256 < 128) {
     // Under half a chip of 256 x 256 tiles: 128 x 128 tiles (two per CU)
     // spread the work over 4x the workgroups, unless the 256 x 256 launch
-    // splits its lone round along K (a long reduction).  E=1, M=2080 (one
+    // splits its lone round along K (a long reduction; judged for the full
+    // workspace that mxgg_grouped_mm_workspace_size recommends).  E=1, M=2080 (one
     // GPU's share of E=8 under 8-way expert parallelism), N=2048: K=5120
     // 77 -> 54 us; K=8192 splits (70 us, against 76 us as 128 x 128).
     const int par = fwd_resident<CfgF8_256>();
