@@ -13,6 +13,9 @@ Per shape and direction:
   * the GPU reference itself pinned to the CPU oracle (oracle.grouped_mm /
     oracle.wgrad, fp64) on a slice: 256 rows across a group boundary x 128
     columns (forward, dgrad), or a 64 x 64 block of every group (wgrad).
+
+The same checks run on the bench's expert-parallel shard: one expert and
+2080 tokens, the nine N, K, forward and wgrad.
 """
 
 import random
@@ -69,12 +72,11 @@ def _check_group(out_g, ref_g, hp_g, what):
         assert sq >= SQNR_GATE, f"{what}: sqnr {sq:.2f} dB"
 
 
-def _nt_case(gpu, E, rows_n, red, offs, seed, what):
+def _nt_case(gpu, E, rows_n, red, offs, seed, what, M=M_TOKENS):
     """out (M, rows_n) = X (M, red) @ W[g]^T (E, rows_n, red) per group: the
     forward (rows_n = N, red = K) and dgrad (grad_out against W^T viewed
     (E, K, N): rows_n = K, red = N) calls."""
     import kernels
-    M = M_TOKENS
     print(f"{what} E={E} M={M} out={rows_n} red={red} offs={list(offs)}", flush=True)
     x = _gen((M, red), 1.0, seed, gpu)
     w = _gen((E, rows_n, red), 0.02, seed + 1, gpu)
@@ -122,12 +124,13 @@ def test_sweep_dgrad(gpu, shape):
 def test_sweep_wgrad(gpu, shape):
     """out[g] (N, K) = grad_out[g]^T @ A[g] over each group's tokens, from
     the dim-1 quantized operands (scales per 32 tokens)."""
-    import kernels
     E, N, K = shape
-    M = M_TOKENS
-    offs = OFFS[shape]
+    _wgrad_case(gpu, E, N, K, OFFS[shape], E * 100 + N + K + 13)
+
+
+def _wgrad_case(gpu, E, N, K, offs, seed, M=M_TOKENS):
+    import kernels
     print(f"wgrad E={E} M={M} N={N} K={K} offs={list(offs)}", flush=True)
-    seed = E * 100 + N + K + 13
     go = _gen((M, N), 1.0, seed, gpu)
     ia = _gen((M, K), 1.0, seed + 1, gpu)
     sg, qg = kernels.to_mx_dim0(go)          # (N, M)
@@ -148,3 +151,24 @@ def test_sweep_wgrad(gpu, shape):
         assert O.rel_fro(ora, ref[n0:n0 + 64, k0:k0 + 64].double().cpu().numpy()) <= REF_PIN
         assert O.rel_fro(ora, out[e, n0:n0 + 64, k0:k0 + 64].float().cpu().numpy()) <= REL_FRO_TIGHT
         del ref, hp
+
+
+# One GPU's share of the E=8 sweep shapes under 8-way expert parallelism
+# (the bench's ep_shard line): one expert, 2080 tokens.  Few tiles, so the
+# small-problem launch rules run here (128 x 128 tiles when a lone 256 x 256
+# round would not split, the split of a lone round with its reduce), and
+# 2080-token rows are not a multiple of 128 bytes (the quantizer pads them).
+EP_M = M_TOKENS // 8
+EP_SHAPES = [(n, k) for n in (2048, 5120, 8192) for k in (2048, 5120, 8192)]
+
+
+@pytest.mark.parametrize("shape", EP_SHAPES, ids=[f"N{n}-K{k}" for n, k in EP_SHAPES])
+def test_ep_shard_fwd(gpu, shape):
+    N, K = shape
+    _nt_case(gpu, 1, N, K, [EP_M], seed=N + K + 3, what="ep fwd", M=EP_M)
+
+
+@pytest.mark.parametrize("shape", EP_SHAPES, ids=[f"N{n}-K{k}" for n, k in EP_SHAPES])
+def test_ep_shard_wgrad(gpu, shape):
+    N, K = shape
+    _wgrad_case(gpu, 1, N, K, [EP_M], N + K + 5, M=EP_M)
