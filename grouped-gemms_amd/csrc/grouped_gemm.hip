@@ -181,10 +181,40 @@ __device__ __forceinline__ int swz4(int r) {
 }
 __device__ __forceinline__ int swz2(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
+// A tile's rows of one operand in global memory, in one of two layouts:
+//   rows  (pl = 0): byte k of row r at r * ld + k;
+//   pairs (pl = 1): rows 2i and 2i+1 interleave in 64-byte pieces, byte k of
+//         row r at (r / 2) * 2 ld + (k / 64) * 128 + (r % 2) * 64 + k % 64,
+//         so the 64-byte stage pieces of two adjacent rows fill one 128-byte
+//         line and a 16-row copy touches 8 whole lines instead of 16 halves.
+// Local row r of the tile is row e = r + shift of the buffer `data`, which
+// starts at the tile's first row (rows) or first pair (pairs: shift = row0 %
+// 2); the range ends after the pair of the tile's last row, so reads past the
+// tile's rows return 0 except the partner row of a last, odd row.
 struct Operand {
-  __amdgpu_buffer_rsrc_t data;   // base = first row of the tile; range = valid rows
-  uint32_t ld;                   // bytes between rows
+  __amdgpu_buffer_rsrc_t data;
+  uint32_t ld;                   // rows: bytes between rows; pairs: half the bytes between pairs
+  uint32_t pl;                   // layout: 0 rows, 1 pairs
+  uint32_t shift;                // pairs: row0 % 2 of the tile; rows: 0
 };
+
+// Operand of rows row0 .. row0 + rows - 1 of the matrix at `base`.
+__device__ __forceinline__ Operand make_operand(const uint8_t* base, int64_t ld, int pl, int64_t row0, int rows) {
+  Operand o;
+  o.ld = (uint32_t)ld;
+  o.pl = (uint32_t)pl;
+  o.shift = (uint32_t)(row0 & pl);
+  const int64_t unit = ld << pl;                                  // bytes per row (pair)
+  const uint32_t units = (uint32_t)(((int64_t)o.shift + rows + pl) >> pl);
+  o.data = make_rsrc(base + (row0 >> pl) * unit, units * (uint32_t)unit);
+  return o;
+}
+
+// Byte offset in O.data of byte `col` of local row `row`.
+__device__ __forceinline__ uint32_t operand_off(const Operand& O, uint32_t row, uint32_t col) {
+  const uint32_t e = row + O.shift;
+  return (e >> O.pl) * (O.ld << O.pl) + ((col >> 6) << (6 + O.pl)) + ((e & O.pl) << 6) + (col & 63u);
+}
 
 // Where a tile's step-major scales live: dword (t, r) of an operand with R
 // rows per step is at byte 4 (t R + r) of the buffer `rsrc` (the operand's
@@ -206,9 +236,9 @@ struct Frags {
 // (q = wave*Q + i; R = 16 rows of 64 bytes, or 32 rows of 32 bytes for packed
 // e2m1 W); the lane's row inside a copy and its swizzled chunk do not depend
 // on i, so one per-lane offset serves all copies and the row step of copy i
-// travels in the scalar offset.  The chunk index rides in bits 28..31 (a
-// lane's offset is at most 31 rows of a stride below 2**23 plus 48 bytes:
-// below 2**28).
+// (R rows: R * ld bytes in either layout, R being even) travels in the scalar
+// offset.  The chunk index rides in bits 28..31 (a lane's offset is at most
+// 31 rows, or 8 pairs, of a stride below 2**23 plus 112 bytes: below 2**28).
 // Scale copy of wave w (w < NSD): slot dwords 256 w .. 256 w + 255, 4 per
 // lane, of the X part (w < NSX) or the W part; lane l covers step u and tile
 // rows r .. r+3 of its operand, at byte s_base + t * s_step of that
@@ -228,16 +258,16 @@ __device__ __forceinline__ void make_plan(Plan<C>& P, const Operand& X, const Op
   {
     const int row = lane / 4;
     const int c = (lane & 3) ^ swz4(row);
-    P.xoff = ((uint32_t)row * X.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
+    P.xoff = operand_off(X, (uint32_t)row, (uint32_t)c * 16u) | ((uint32_t)c << 28);
   }
   if constexpr (C::F4) {
     const int row = lane / 2;
     const int c = (lane & 1) ^ swz2(row);
-    P.woff = ((uint32_t)row * W.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
+    P.woff = operand_off(W, (uint32_t)row, (uint32_t)c * 16u) | ((uint32_t)c << 28);
   } else {
     const int row = lane / 4;
     const int c = (lane & 3) ^ swz4(row);
-    P.woff = ((uint32_t)row * W.ld + (uint32_t)c * 16u) | ((uint32_t)c << 28);
+    P.woff = operand_off(W, (uint32_t)row, (uint32_t)c * 16u) | ((uint32_t)c << 28);
   }
   const int wave = wave_id();
   const bool isx = wave < C::NSX;
@@ -271,14 +301,14 @@ __device__ __forceinline__ void issue_stage(uint8_t* sb, const Operand& X, const
 #pragma unroll
   for (int i = 0; i < C::QX; ++i) {
     const int q = wave * C::QX + i;
-    const uint32_t so = (uint32_t)st * C::XROW + (uint32_t)(q * 16) * X.ld;
+    const uint32_t so = ((uint32_t)st * C::XROW << X.pl) + (uint32_t)(q * 16) * X.ld;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(X.data, (lds_ptr_t)(sb + q * 1024), 16, xo, so, 0, 0);
   }
   uint8_t* wb = sb + C::XBYTES;
 #pragma unroll
   for (int i = 0; i < C::QW; ++i) {
     const int q = wave * C::QW + i;
-    const uint32_t so = (uint32_t)st * C::WROW + (uint32_t)(q * WR) * W.ld;
+    const uint32_t so = ((uint32_t)st * C::WROW << W.pl) + (uint32_t)(q * WR) * W.ld;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(W.data, (lds_ptr_t)(wb + q * 1024), 16, wo, so, 0, 0);
   }
 }
@@ -554,7 +584,8 @@ __device__ __forceinline__ void edge_chunk(const Operand& X, const Operand& W, c
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) {
     const uint32_t row = (uint32_t)(wm * C::WTM + i * 32 + r32);
-    const v4i v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(X.data, row * X.ld + cs, 0, 0));
+    const v4i v =
+        __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(X.data, operand_off(X, row, (uint32_t)cs), 0, 0));
     v8i f = (v8i){0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -568,7 +599,8 @@ __device__ __forceinline__ void edge_chunk(const Operand& X, const Operand& W, c
 #pragma unroll
   for (int j = 0; j < C::FN; ++j) {
     const uint32_t row = (uint32_t)(wn * C::WTN + j * 32 + r32);
-    const v4i v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(W.data, row * W.ld + cs, 0, 0));
+    const v4i v =
+        __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(W.data, operand_off(W, row, (uint32_t)cs), 0, 0));
     v8i f = (v8i){0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -894,6 +926,7 @@ struct FwdParams {
   int grid_n; int group_m; int xcd;
   float* part; int par; int slots;          // split: partial slots, resident workgroups, slot count
   int quads;                                // last round as 128 x 128 quarter tiles (quad_dp)
+  int a_pl; int b_pl;                       // operand layouts: 0 rows, 1 row pairs (Operand)
 };
 
 // Epilogue of the whole-tile kernels, fixed at compile time so that the
@@ -971,11 +1004,8 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
   const int64_t row0 = tl.row0, n0 = tl.n0;
   const int rows = tl.rows, cols = tl.cols;
 
-  Operand X, W;
-  X.ld = (uint32_t)p.lda;
-  X.data = make_rsrc(p.a + row0 * p.lda, (uint32_t)rows * X.ld);
-  W.ld = (uint32_t)p.ldb_n;
-  W.data = make_rsrc(p.b + (int64_t)tl.expert * p.ldb_e + n0 * p.ldb_n, (uint32_t)cols * W.ld);
+  const Operand X = make_operand(p.a, p.lda, p.a_pl, row0, rows);
+  const Operand W = make_operand(p.b + (int64_t)tl.expert * p.ldb_e, p.ldb_n, p.b_pl, n0, cols);
   const ScaleSrc xs{make_rsrc(p.as, p.as_bytes), (uint32_t)p.M, (uint32_t)row0};
   const ScaleSrc ws{make_rsrc(p.bs + (int64_t)tl.expert * p.bs_expert, p.bs_expert), (uint32_t)p.N, (uint32_t)n0};
 
@@ -1156,6 +1186,7 @@ struct WgradParams {
   int tiles_n; int tiles_k;
   float* part; int dp; int S; int units;    // split plan (host): see split_plan
   int dev; int par; int slots;              // dev: plan on the device (wgrad_groups / wgrad_plan) from par, slots
+  int go_pl; int ia_pl;                     // operand layouts: 0 rows, 1 row pairs (Operand)
 };
 
 struct WgradTile {
@@ -1398,11 +1429,8 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
     if (STEP * b < hi) hi = STEP * b;
   }
 
-  Operand X, W;
-  X.ld = (uint32_t)p.ld_go;
-  X.data = make_rsrc(p.go + n0 * p.ld_go, (uint32_t)rows * X.ld);
-  W.ld = (uint32_t)p.ld_ia;
-  W.data = make_rsrc(p.ia + k0 * p.ld_ia, (uint32_t)cols * W.ld);
+  const Operand X = make_operand(p.go, p.ld_go, p.go_pl, n0, rows);
+  const Operand W = make_operand(p.ia, p.ld_ia, p.ia_pl, k0, cols);
   const ScaleSrc xs{make_rsrc(p.gs, p.gs_bytes), (uint32_t)p.N, (uint32_t)n0};
   const ScaleSrc ws{make_rsrc(p.is, p.is_bytes), (uint32_t)p.K, (uint32_t)k0};
 
@@ -1805,24 +1833,37 @@ extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, in
   return part ? align256(sc) + part : sc;
 }
 
+// Bytes a row of `len` bytes takes in an operand of layout flag `pairs`: the
+// row-pair layout stores whole 64-byte pieces.
+static int64_t operand_row_bytes(int64_t len, bool pairs) { return pairs ? (len + 63) / 64 * 64 : len; }
+
 // Argument checks of a forward call shared by the entry points; MXGG_OK
 // when the call may go ahead (check *empty: nothing to compute).
 // plain: A_s / B_s are plain scales with these strides (else step-major,
-// strides unused).
+// strides unused).  layout: MXGG_A_PAIRS / MXGG_B_PAIRS flags.
 static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas, const uint8_t* B,
                             int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
                             int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
-                            const void* out, int out_dtype, int64_t ldo, bool plain, bool* empty) {
+                            const void* out, int out_dtype, int64_t ldo, bool plain, int layout, bool* empty) {
   *empty = false;
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: weight format %d not E4M3/E2M1", b_fmt);
+  if (layout & ~(MXGG_A_PAIRS | MXGG_B_PAIRS))
+    return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: unknown operand layout flags %d", layout);
+  const bool ap = layout & MXGG_A_PAIRS, bp = layout & MXGG_B_PAIRS;
+  if (bp && b_fmt != MXGG_FMT_E4M3)
+    return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: row pairs are built for e4m3 weights only");
+  if ((ap && M % 2) || (bp && N % 2))
+    return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: an operand in row pairs needs an even row count (M=%lld, N=%lld)",
+                (long long)M, (long long)N);
   if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F16 && out_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: out_dtype %d not BF16/F16/F32", out_dtype);
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: E=%d out of range", E);
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: negative shape");
   if (K % 32) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: K=%lld must be a multiple of 32", (long long)K);
   const int64_t kb = b_fmt == MXGG_FMT_E2M1 ? K / 2 : K;
-  if (lda < K || ldb_n < kb || ldo < N || (plain && (ldas < K / 32 || ldbs_n < K / 32)))
+  if (lda < operand_row_bytes(K, ap) || ldb_n < operand_row_bytes(kb, bp) || ldo < N ||
+      (plain && (ldas < K / 32 || ldbs_n < K / 32)))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: a row stride is smaller than its row");
   if (E > 1 && (ldb_e < N * ldb_n || (plain && ldbs_e < N * ldbs_n)))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: expert stride smaller than one expert");
@@ -1849,7 +1890,7 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
 static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, const uint8_t* B, int b_fmt,
                              int64_t ldb_n, int64_t ldb_e, const uint8_t* bs, const int32_t* offs, int E, int64_t M,
                              int64_t N, int64_t K, void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
-                             int group_m, int xcd, void* part_area, size_t part_bytes, hipStream_t st) {
+                             int group_m, int xcd, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
   FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
   const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
                                            : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
@@ -1857,7 +1898,8 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
   const int64_t T = cdiv(K, STEP);
   float* part = c.split && part_area && part_bytes ? (float*)part_area : nullptr;
   FwdParams p{A, lda, B, ldb_n, ldb_e, as, (uint32_t)(4 * T * M), bs, (uint32_t)(4 * T * N), offs, E, M, N, K,
-              (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0};
+              (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0, 0,
+              (layout & MXGG_A_PAIRS) ? 1 : 0, (layout & MXGG_B_PAIRS) ? 1 : 0};
   const size_t pb = part ? part_bytes : 0;
   if (b_fmt == MXGG_FMT_E2M1)
     return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
@@ -1887,7 +1929,7 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
   const size_t part_off = align256(need);
   void* part = ws_bytes > part_off ? (void*)((uint8_t*)workspace + part_off) : nullptr;
   return launch_grouped_mm(A, lda, (const uint8_t*)wsd, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)(wsd + T * M), offs,
-                           E, M, N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, part,
+                           E, M, N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, 0, part,
                            part ? ws_bytes - part_off : 0, st);
 }
 
@@ -1900,7 +1942,7 @@ extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s
   clear_error();
   bool empty;
   if (int rc = check_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
-                                out, out_dtype, ldo, true, &empty))
+                                out, out_dtype, ldo, true, 0, &empty))
     return rc;
   if (empty) return MXGG_OK;
   const size_t need = fwd_scale_bytes(E, M, N, K);
@@ -1916,18 +1958,18 @@ extern "C" int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32
                                      int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint32_t* B_ss,
                                      const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
                                      int out_dtype, int64_t ldo, int block_m, int block_n, int group_m, int xcd,
-                                     void* workspace, size_t ws_bytes, void* stream) {
+                                     int layout, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
   bool empty;
   if (int rc = check_grouped_mm(A, lda, (const uint8_t*)A_ss, 0, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)B_ss, 0, 0,
-                                offs, E, M, N, K, out, out_dtype, ldo, false, &empty))
+                                offs, E, M, N, K, out, out_dtype, ldo, false, layout, &empty))
     return rc;
   if (empty) return MXGG_OK;
   if (((uintptr_t)A_ss | (uintptr_t)B_ss) & 3)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_steps: step-major scales must be 4-byte aligned");
   if (int rc = require_device()) return rc;
   return launch_grouped_mm(A, lda, (const uint8_t*)A_ss, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)B_ss, offs, E, M,
-                           N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, workspace,
+                           N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, layout, workspace,
                            workspace ? ws_bytes : 0, (hipStream_t)stream);
 }
 
@@ -1978,7 +2020,7 @@ extern "C" int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint
   clear_error();
   bool empty;
   if (int rc = check_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K,
-                                out, out_dtype, ldo, true, &empty))
+                                out, out_dtype, ldo, true, 0, &empty))
     return rc;
   if (empty) return MXGG_OK;
   const size_t need = fwd_scale_bytes(E, M, N, K);
@@ -2039,14 +2081,21 @@ extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t
 // these strides); *empty: nothing to compute.
 static int check_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos, const uint8_t* ia_t,
                        int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias, const int32_t* offs, int E, int64_t M,
-                       int64_t N, int64_t K, const void* out, int out_dtype, bool plain, bool* empty) {
+                       int64_t N, int64_t K, const void* out, int out_dtype, bool plain, int layout, bool* empty) {
   *empty = false;
   if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: out_dtype %d not BF16/F32", out_dtype);
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "wgrad: E=%d out of range", E);
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "wgrad: negative shape");
   if (M % 32) return fail(MXGG_ERR_INVALID_ARG, "wgrad: M=%lld must be a multiple of 32", (long long)M);
-  if (ld_go < M || ld_ia < M || (plain && (ld_gos < M / 32 || ld_ias < M / 32)))
+  if (layout & ~(MXGG_A_PAIRS | MXGG_B_PAIRS))
+    return fail(MXGG_ERR_INVALID_ARG, "wgrad: unknown operand layout flags %d", layout);
+  const bool gp = layout & MXGG_A_PAIRS, ip = layout & MXGG_B_PAIRS;
+  if ((gp && N % 2) || (ip && K % 2))
+    return fail(MXGG_ERR_INVALID_ARG, "wgrad: an operand in row pairs needs an even row count (N=%lld, K=%lld)",
+                (long long)N, (long long)K);
+  if (ld_go < operand_row_bytes(M, gp) || ld_ia < operand_row_bytes(M, ip) ||
+      (plain && (ld_gos < M / 32 || ld_ias < M / 32)))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: a row stride is smaller than its row");
   if (ld_go % 16 || ld_ia % 16 || !aligned16(go_t) || !aligned16(ia_t))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: operand rows must be 16-byte aligned");
@@ -2069,12 +2118,13 @@ static int check_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, 
 // of tiles cut along the tokens (none: no tile is cut).
 static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, const uint8_t* ia_t, int64_t ld_ia,
                         const uint8_t* is, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
-                        int out_dtype, void* part_area, size_t part_bytes, hipStream_t st) {
+                        int out_dtype, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
   typedef CfgF8_256 C;
   const int64_t T = cdiv(M, STEP);
   float* part = part_area && part_bytes ? (float*)part_area : nullptr;
   WgradParams p{go_t, ld_go, ia_t, ld_ia, gs, (uint32_t)(4 * T * N), is, (uint32_t)(4 * T * K), offs, E, M, N, K,
-                (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0, 0, 0, 0};
+                (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0, 0, 0, 0,
+                (layout & MXGG_A_PAIRS) ? 1 : 0, (layout & MXGG_B_PAIRS) ? 1 : 0};
   const int64_t tiles = (int64_t)E * p.tiles_n * p.tiles_k;
   if (tiles > INT32_MAX / 2) return fail(MXGG_ERR_UNSUPPORTED, "wgrad: grid too large");
   static int resident_cache[64];
@@ -2124,7 +2174,7 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   clear_error();
   bool empty;
   if (int rc = check_wgrad(go_t, ld_go, go_s, ld_gos, ia_t, ld_ia, ia_s, ld_ias, offs, E, M, N, K, out, out_dtype,
-                           true, &empty))
+                           true, 0, &empty))
     return rc;
   if (empty) return MXGG_OK;
   const size_t need = wgrad_scale_bytes(M, N, K);
@@ -2143,22 +2193,22 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   const size_t part_off = align256(need);
   void* part = ws_bytes > part_off ? (void*)((uint8_t*)workspace + part_off) : nullptr;
   return launch_wgrad(go_t, ld_go, (const uint8_t*)wsd, ia_t, ld_ia, (const uint8_t*)(wsd + T * N), offs, E, M, N, K,
-                      out, out_dtype, part, part ? ws_bytes - part_off : 0, st);
+                      out, out_dtype, 0, part, part ? ws_bytes - part_off : 0, st);
 }
 
 extern "C" int mxgg_wgrad_steps(const uint8_t* go_t, int64_t ld_go, const uint32_t* go_ss, const uint8_t* ia_t,
                                 int64_t ld_ia, const uint32_t* ia_ss, const int32_t* offs, int E, int64_t M,
-                                int64_t N, int64_t K, void* out, int out_dtype, void* workspace, size_t ws_bytes,
-                                void* stream) {
+                                int64_t N, int64_t K, void* out, int out_dtype, int layout, void* workspace,
+                                size_t ws_bytes, void* stream) {
   clear_error();
   bool empty;
   if (int rc = check_wgrad(go_t, ld_go, (const uint8_t*)go_ss, 0, ia_t, ld_ia, (const uint8_t*)ia_ss, 0, offs, E, M,
-                           N, K, out, out_dtype, false, &empty))
+                           N, K, out, out_dtype, false, layout, &empty))
     return rc;
   if (empty) return MXGG_OK;
   if (((uintptr_t)go_ss | (uintptr_t)ia_ss) & 3)
     return fail(MXGG_ERR_INVALID_ARG, "wgrad_steps: step-major scales must be 4-byte aligned");
   if (int rc = require_device()) return rc;
   return launch_wgrad(go_t, ld_go, (const uint8_t*)go_ss, ia_t, ld_ia, (const uint8_t*)ia_ss, offs, E, M, N, K, out,
-                      out_dtype, workspace, workspace ? ws_bytes : 0, (hipStream_t)stream);
+                      out_dtype, layout, workspace, workspace ? ws_bytes : 0, (hipStream_t)stream);
 }

@@ -27,6 +27,13 @@
 // for batches of R rows, dword (b, t, r) holds blocks 4t .. 4t+3 of row
 // b*R + r, bytes past the row's last block 127), so a GEMM given them skips
 // its per-call re-layout.
+//
+// E4M3 data goes out row-major or, on request (MXGG_DATA_PAIRS), in row
+// pairs: byte k of row r at (r/2) 2 ld + (k/64) 128 + (r%2) 64 + k%64, the
+// layout in which the GEMM's 64-element stage of two adjacent rows is one
+// 128-byte line.  Every store of these kernels (8 or 32 bytes at a multiple
+// of its size) stays inside one 64-byte piece, so only the address changes;
+// the pad of a row whose length is an odd multiple of 32 is written zero.
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
@@ -80,6 +87,17 @@ __device__ __forceinline__ uint32_t gather4(uint32_t s, int j) {
   v |= (uint32_t)__shfl_xor((int)v, 1, 4);
   v |= (uint32_t)__shfl_xor((int)v, 2, 4);
   return v;
+}
+
+// Offset of byte k of row r of a quantizer output with row stride ld, row
+// pairs when pl = 1 (k % 64 + the store's size <= 64).
+__device__ __forceinline__ int64_t q_off(int64_t r, int64_t k, int64_t ld, int pl) {
+  return pl ? (r >> 1) * (ld << 1) + ((k >> 6) << 7) + ((r & 1) << 6) + (k & 63) : r * ld + k;
+}
+
+__device__ __forceinline__ void zero32(uint8_t* dst) {
+  *reinterpret_cast<uint4*>(dst) = make_uint4(0, 0, 0, 0);
+  *reinterpret_cast<uint4*>(dst + 16) = make_uint4(0, 0, 0, 0);
 }
 
 // 16 source bytes, read once: a non-temporal load, which leaves the lines
@@ -188,12 +206,13 @@ __device__ __forceinline__ uint32_t quant32(const float (&v)[32], uint8_t* dst) 
 // contiguous 4 KB of bf16), one grid-stride pass per 64 * gridDim.x blocks.
 // When rows hold a multiple of 4 blocks, four consecutive quads' scale bytes
 // (one step of a row) go out as one dword.  I: the block index type (32-bit
-// when the block count fits: one cheap division per block).
+// when the block count fits: one cheap division per block).  pl: e4m3 output
+// in row pairs.
 template <int SRC, int FMT, class I>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restrict__ src,
                                                          int64_t rows, int64_t cols,
                                                          int64_t ld_src_bytes,
-                                                         uint8_t* __restrict__ q, int64_t ld_q,
+                                                         uint8_t* __restrict__ q, int64_t ld_q, int pl,
                                                          ScaleOut so) {
   const I bpr = (I)(cols / 32);                        // blocks per row
   const I nblk = (I)rows * bpr;
@@ -228,7 +247,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restri
           lo = e4m3x4(v[0], v[1], v[2], v[3], mul);
           hi = e4m3x4(v[4], v[5], v[6], v[7], mul);
         }
-        *reinterpret_cast<uint2*>(q + (int64_t)r * ld_q + col) = make_uint2(lo, hi);
+        *reinterpret_cast<uint2*>(q + q_off(r, col, ld_q, pl)) = make_uint2(lo, hi);
+        // row pairs, odd block count: the last block's lanes zero the pad
+        if (pl && (bpr & 1) && cb == bpr - 1)
+          *reinterpret_cast<uint2*>(q + q_off(r, col + 32, ld_q, pl)) = make_uint2(0, 0);
       } else {
         uint32_t w = 0;
 #pragma unroll
@@ -261,11 +283,12 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restri
 // 128-byte output lines and the group's four scale bytes leave as one dword.
 // In LDS, 32-row band k of the tile is rotated by 16k columns, so the four
 // lanes of a group, reading four bands of one column, hit disjoint banks.
-// rows % 32 == 0: a partial last tile has whole 32-row blocks.
+// rows % 32 == 0: a partial last tile has whole 32-row blocks.  pl: outputs
+// in row pairs (rows and cols even, so a batch is whole pairs).
 template <int SRC, bool ROWS>
 __global__ __launch_bounds__(256) void quant_tile_kernel(
     const uint8_t* __restrict__ src, int64_t rows, int64_t cols, int64_t ld_src_bytes, uint8_t* __restrict__ q_r,
-    int64_t ld_qr, ScaleOut s_r, uint8_t* __restrict__ q_c, int64_t ld_qc, ScaleOut s_c) {
+    int64_t ld_qr, ScaleOut s_r, uint8_t* __restrict__ q_c, int64_t ld_qc, ScaleOut s_c, int pl) {
   constexpr int EB = elem_bytes<SRC>();
   constexpr int T = 128;                              // tile rows and columns
   constexpr int PITCH = T * EB + 16;                  // LDS row pitch, bytes
@@ -312,7 +335,9 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(
         float v[32];
 #pragma unroll
         for (int i = 0; i < 32; ++i) v[i] = elem_to_f32<SRC>(&tile[at(32 * j + i, c)]);
-        sc = quant32(v, q_c + (c0 + c) * ld_qc + r0 + 32 * j);
+        sc = quant32(v, q_c + q_off(c0 + c, r0 + 32 * j, ld_qc, pl));
+      } else if (pl && j == bands && (bands & 1)) {
+        zero32(q_c + q_off(c0 + c, r0 + 32 * j, ld_qc, pl));   // pad of a row of 64k + 32 bytes
       }
       const uint32_t w4 = gather4(sc, j);
       if (j == 0) put_scale4(s_c, b * cols + c0 + c, r0 / 32, w4, bands < 4 ? bands : 4);
@@ -335,7 +360,9 @@ __global__ __launch_bounds__(256) void quant_tile_kernel(
 #pragma unroll
             for (int e = 0; e < EPC; ++e) v[k + e] = elem_to_f32<SRC>(cp + e * EB);
           }
-          sc = quant32(v, q_r + (r0 + r) * ld_qr + c0 + 32 * j);
+          sc = quant32(v, q_r + q_off(r0 + r, c0 + 32 * j, ld_qr, pl));
+        } else if (pl && j == nb && (nb & 1)) {
+          zero32(q_r + q_off(r0 + r, c0 + 32 * j, ld_qr, pl));
         }
         const uint32_t w4 = gather4(sc, j);
         if (j == 0) put_scale4(s_r, b * rows + r0 + r, c0 / 32, w4, nb < 4 ? nb : 4);
@@ -353,8 +380,9 @@ namespace {
 // Scale destination for `out_rows` rows of `nblk` blocks; MXGG_OK or a
 // failure naming `what`.
 int scale_out(const char* what, uint8_t* p, int64_t ld_s, int layout, int64_t out_rows, int64_t nblk, ScaleOut* o) {
-  if (layout != MXGG_SCALES_PLAIN && layout != MXGG_SCALES_STEPS)
-    return fail(MXGG_ERR_INVALID_ARG, "%s: scale_layout %d not PLAIN/STEPS", what, layout);
+  if (layout & ~(MXGG_SCALES_STEPS | MXGG_DATA_PAIRS))
+    return fail(MXGG_ERR_INVALID_ARG, "%s: layout %d not PLAIN/STEPS, optionally | DATA_PAIRS", what, layout);
+  layout &= MXGG_SCALES_STEPS;
   o->p = p;
   o->ld = ld_s;
   o->T = (nblk + 3) / 4;
@@ -367,6 +395,16 @@ int scale_out(const char* what, uint8_t* p, int64_t ld_s, int layout, int64_t ou
                 (long long)out_rows);
   }
   if (nblk > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "%s: rows too long", what);
+  return MXGG_OK;
+}
+
+// A data output of `rows` rows of `len` bytes in row pairs: even rows, row
+// stride a multiple of 64 that holds the row rounded up to 64.
+int pairs_out(const char* what, int64_t rows, int64_t len, int64_t ld) {
+  if (rows % 2) return fail(MXGG_ERR_INVALID_ARG, "%s: row pairs need an even row count, got %lld", what, (long long)rows);
+  if (ld % 64 || ld < (len + 63) / 64 * 64)
+    return fail(MXGG_ERR_INVALID_ARG, "%s: row pairs need a row stride that is a multiple of 64 and holds %lld bytes",
+                what, (long long)((len + 63) / 64 * 64));
   return MXGG_OK;
 }
 
@@ -388,6 +426,11 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: row stride smaller than the row");
   ScaleOut so;
   if (int rc = scale_out("quantize_mx", scales, ld_s, scale_layout, rows, cols / 32, &so)) return rc;
+  const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : 0;
+  if (pl && elem_fmt != MXGG_FMT_E4M3) return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx: row pairs are built for e4m3 only");
+  if (pl) {
+    if (int rc = pairs_out("quantize_mx", rows, cols, ld_q)) return rc;
+  }
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q || !scales) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: null pointer");
   if (((uintptr_t)src % 16) || ((ld_src * eb) % 16))
@@ -409,10 +452,10 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
   do {                                                                                                     \
     if (small)                                                                                             \
       hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT, uint32_t>), dim3(grid), dim3(256), 0, st, s8, rows,  \
-                         cols, lsb, q8, ld_q, so);                                                         \
+                         cols, lsb, q8, ld_q, pl, so);                                                     \
     else                                                                                                   \
       hipLaunchKernelGGL((quant_rows_kernel<SRC, FMT, int64_t>), dim3(grid), dim3(256), 0, st, s8, rows,   \
-                         cols, lsb, q8, ld_q, so);                                                         \
+                         cols, lsb, q8, ld_q, pl, so);                                                     \
   } while (0)
   if (elem_fmt == MXGG_FMT_E4M3) {
     if (src_dtype == MXGG_DTYPE_BF16) MXGG_QROWS(MXGG_DTYPE_BF16, MXGG_FMT_E4M3);
@@ -442,6 +485,10 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: row stride smaller than the row");
   ScaleOut so;
   if (int rc = scale_out("quantize_mx_dim0", scales, ld_s, scale_layout, cols, rows / 32, &so)) return rc;
+  const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : 0;
+  if (pl) {
+    if (int rc = pairs_out("quantize_mx_dim0", cols, rows, ld_q)) return rc;
+  }
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q || !scales) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: null pointer");
   if (((uintptr_t)src % 16) || ((ld_src * eb) % 16) || ((cols * eb) % 16))
@@ -457,7 +504,7 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
   const ScaleOut none{};
 #define MXGG_QCOLS(SRC) \
   hipLaunchKernelGGL((quant_tile_kernel<SRC, false>), grid, dim3(256), 0, st, s8, rows, cols, lsb, nullptr, 0, none, \
-                     (uint8_t*)q, ld_q, so)
+                     (uint8_t*)q, ld_q, so, pl)
   if (src_dtype == MXGG_DTYPE_BF16) MXGG_QCOLS(MXGG_DTYPE_BF16);
   else if (src_dtype == MXGG_DTYPE_F16) MXGG_QCOLS(MXGG_DTYPE_F16);
   else MXGG_QCOLS(MXGG_DTYPE_F32);
@@ -481,6 +528,11 @@ extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t bat
   ScaleOut sr, sc;
   if (int rc = scale_out("quantize_mx_both", s_rows, ld_sr, scale_layout, batch * rows, cols / 32, &sr)) return rc;
   if (int rc = scale_out("quantize_mx_both", s_cols, ld_sc, scale_layout, batch * cols, rows / 32, &sc)) return rc;
+  const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : 0;
+  if (pl) {
+    if (int rc = pairs_out("quantize_mx_both", rows, cols, ld_qr)) return rc;
+    if (int rc = pairs_out("quantize_mx_both", cols, rows, ld_qc)) return rc;
+  }
   if (batch == 0 || rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q_rows || !s_rows || !q_cols || !s_cols)
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_both: null pointer");
@@ -498,7 +550,7 @@ extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t bat
   const int64_t lsb = ld_src * eb;
 #define MXGG_QBOTH(SRC)                                                                                  \
   hipLaunchKernelGGL((quant_tile_kernel<SRC, true>), grid, dim3(256), 0, st, s8, rows, cols, lsb,         \
-                     (uint8_t*)q_rows, ld_qr, sr, (uint8_t*)q_cols, ld_qc, sc)
+                     (uint8_t*)q_rows, ld_qr, sr, (uint8_t*)q_cols, ld_qc, sc, pl)
   if (src_dtype == MXGG_DTYPE_BF16) MXGG_QBOTH(MXGG_DTYPE_BF16);
   else if (src_dtype == MXGG_DTYPE_F16) MXGG_QBOTH(MXGG_DTYPE_F16);
   else MXGG_QBOTH(MXGG_DTYPE_F32);

@@ -6,11 +6,13 @@ Drop-in for the reference package ``kernels`` (kernels/__init__.py:17-25):
   - ``triton_mxfp8_wgrad``: weight-gradient grouped GEMM (A^T @ B per group)
   - ``_rocm_mxfp8_available``: True when the native library is loadable on ROCm
 
-plus the on-GPU quantizers ``to_mx`` / ``to_mx_dim0`` (the reference quantizes
-with eager torch ops in utils.py:67-105).
+plus the on-GPU quantizers ``to_mx`` / ``to_mx_dim0`` / ``to_mx_both`` (the
+reference quantizes with eager torch ops in utils.py:67-105), whose
+``data_layout="pairs"`` output (or ``to_row_pairs`` of row-major data) the
+GEMMs copy in whole 128-byte lines.
 """
 
-from ._common import _rocm_mxfp8_available
+from ._common import _rocm_mxfp8_available, to_row_pairs
 from .backward import triton_mxfp8_wgrad
 from .forward import triton_mxfp8_grouped_mm
 from .moe import MXFP8GroupedLinear, mxfp8_grouped_mm
@@ -23,6 +25,7 @@ __all__ = [
     "to_mx",
     "to_mx_dim0",
     "to_mx_both",
+    "to_row_pairs",
     "mxfp8_grouped_mm",
     "MXFP8GroupedLinear",
 ]

@@ -29,6 +29,9 @@ DTYPE_F16 = 1
 DTYPE_F32 = 2
 SCALES_PLAIN = 0
 SCALES_STEPS = 1
+DATA_PAIRS = 2      # quantizer data outputs in row pairs (OR-ed into the scale layout)
+A_PAIRS = 1         # *_steps GEMMs: A / go_t in row pairs
+B_PAIRS = 2         # *_steps GEMMs: B / ia_t in row pairs
 
 _c_i32 = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -62,7 +65,7 @@ SIGNATURES = {
                                        _c_p, _c_i32, _c_i64, _c_i64, _c_p,
                                        _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
                                        _c_p, _c_i32, _c_i64,
-                                       _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
+                                       _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
     "mxgg_grouped_mm_noalloc": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
                                          _c_p, _c_i32, _c_i64, _c_i64,
                                          _c_p, _c_i64, _c_i64,
@@ -79,7 +82,7 @@ SIGNATURES = {
                             _c_p, _c_i32, _c_p, _c_sz, _c_p]),
     "mxgg_wgrad_steps": (_c_i32, [_c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p,
                                   _c_p, _c_i32, _c_i64, _c_i64, _c_i64,
-                                  _c_p, _c_i32, _c_p, _c_sz, _c_p]),
+                                  _c_p, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
 }
 
 _lock = threading.Lock()

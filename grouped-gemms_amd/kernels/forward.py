@@ -14,7 +14,11 @@ Beyond the reference, the weight may be MXFP4: ``weight`` of dtype
 byte (element 2i in the low nibble), scales per 32 elements of K.  And the
 scales may come step-major (int32 ``(T, M)`` and ``(E, T, N)``,
 ``T = cdiv(K, 128)``, as ``to_mx(..., scale_layout="steps")`` writes them):
-the call then skips the re-layout launch (``mxgg_grouped_mm_steps``).
+the call then skips the re-layout launch (``mxgg_grouped_mm_steps``).  With
+step-major scales either e4m3 operand may also be in row pairs (the view
+``(M/2, 2, cdiv(K, 64), 64)``, resp. ``(E, N/2, 2, cdiv(K, 64), 64)``, that
+``to_mx(..., data_layout="pairs")`` returns), which the kernels copy in whole
+128-byte lines.
 """
 
 from __future__ import annotations
@@ -22,7 +26,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._common import _offsets, _out_code, _require, _rowmajor, _stream_handle, _u8
+from ._common import _offsets, _out_code, _pair_geometry, _require, _rowmajor, _stream_handle, _u8
 
 # Tile shapes built into libmxgg (BLOCK_M x BLOCK_N); BLOCK_K is fixed at 128.
 BUILT_TILES = ((256, 256), (128, 128))
@@ -93,25 +97,43 @@ def triton_mxfp8_grouped_mm(
 
     Returns ``(M, N)`` of ``out_dtype``; rows at or past ``offs[-1]`` are left
     uninitialised, as in the reference.
+
+    Row-pair operands (see the module doc; step-major scales only) span K
+    rounded up to 64.  With one of them row-major its K is used, and the bits
+    equal the all-row-major call's.  With both in row pairs the call runs at
+    the rounded K: for K % 64 == 32 that adds 32 zeros with scale 2**0 to
+    every dot product (the quantizers zero the pad), which the kernels do
+    anyway, but the launch configuration is the one chosen for the rounded K.
     """
     _require(input_act, "input_act")
-    M, K = input_act.shape
-    E, N, K2 = weight.shape
-    if weight.dtype == torch.float8_e4m3fn:
-        b_fmt = _lib.FMT_E4M3
-        assert K == K2, f"K mismatch: A={K}, B={K2}"
-    elif weight.dtype in _FP4_DTYPES:
-        b_fmt = _lib.FMT_E2M1
-        assert K == 2 * K2, f"K mismatch: A={K}, packed fp4 B={K2} (K/2 expected)"
-    else:
-        raise TypeError(f"weight dtype {weight.dtype} is neither float8_e4m3fn nor packed fp4")
     if input_act.dtype != torch.float8_e4m3fn:
         raise TypeError(f"input_act dtype {input_act.dtype} is not float8_e4m3fn")
+    pa = _pair_geometry(input_act, 0)
+    pb = _pair_geometry(weight, 1) if weight.dtype == torch.float8_e4m3fn else None
+    M, Ka = (pa[0], pa[1]) if pa else input_act.shape
+    if weight.dtype == torch.float8_e4m3fn:
+        b_fmt = _lib.FMT_E4M3
+        E, N, Kb = (weight.shape[0], pb[0], pb[1]) if pb else weight.shape
+    elif weight.dtype in _FP4_DTYPES:
+        b_fmt = _lib.FMT_E2M1
+        E, N, Kb = weight.shape[0], weight.shape[1], 2 * weight.shape[2]
+    else:
+        raise TypeError(f"weight dtype {weight.dtype} is neither float8_e4m3fn nor packed fp4")
+    # K: the row-major operand's (row pairs round it up to 64)
+    K = Kb if pa and not pb else Ka
+    pad = (pa or pb)[1] if (pa is None) != (pb is None) else None
+    if pad is not None:
+        assert (K + 63) // 64 * 64 == pad, f"K mismatch: {K} and row pairs of {pad} bytes"
+    else:
+        assert Ka == Kb, f"K mismatch: A={Ka}, B={Kb}" + (" (packed fp4: K/2 bytes)" if b_fmt else "")
     if K % 32:
         raise ValueError(f"K={K} must be a multiple of the MX block size 32")
     steps = input_act_scales.dtype == torch.int32
     if steps != (weight_scales.dtype == torch.int32):
         raise TypeError("input_act_scales and weight_scales must both be e8m0 bytes or both step-major int32")
+    layout = (_lib.A_PAIRS if pa else 0) | (_lib.B_PAIRS if pb else 0)
+    if layout and not steps:
+        raise TypeError("row-pair operands need step-major int32 scales (scale_layout='steps')")
     T = (K + 127) // 128
     want_a, want_b = ((T, M), (E, T, N)) if steps else ((M, K // 32), (E, N, K // 32))
     if tuple(input_act_scales.shape) != want_a:
@@ -128,8 +150,10 @@ def triton_mxfp8_grouped_mm(
     if (bm, bn) not in BUILT_TILES:
         bm = bn = 0
     dev = input_act.device
-    a = _u8(_rowmajor(input_act))
-    b = _u8(_rowmajor(weight))
+    a = _u8(input_act if pa else _rowmajor(input_act))
+    b = _u8(weight if pb else _rowmajor(weight))
+    lda = pa[2] if pa else a.stride(0)
+    ldb_n = pb[2] if pb else b.stride(1)
     offs = _offsets(group_end_offsets, dev)
     out = torch.empty((M, N), dtype=out_dtype, device=dev)
     code = _out_code(out_dtype)
@@ -143,11 +167,11 @@ def triton_mxfp8_grouped_mm(
         ws_bytes = _split_room(ws_bytes, 4 * T * (M + E * N))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         rc = lib.mxgg_grouped_mm_steps(
-            a.data_ptr(), a.stride(0), a_ss.data_ptr(),
-            b.data_ptr(), b_fmt, b.stride(1), b.stride(0), b_ss.data_ptr(),
+            a.data_ptr(), lda, a_ss.data_ptr(),
+            b.data_ptr(), b_fmt, ldb_n, b.stride(0), b_ss.data_ptr(),
             offs.data_ptr(), E, M, N, K,
             out.data_ptr(), code, out.stride(0),
-            int(bm), int(bn), int(GROUP_M or 0), int(XCD_SWIZZLE or 0),
+            int(bm), int(bn), int(GROUP_M or 0), int(XCD_SWIZZLE or 0), layout,
             ws.data_ptr() if ws is not None else None, ws_bytes,
             _stream_handle(dev))
         _lib.check(rc)

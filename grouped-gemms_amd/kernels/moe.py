@@ -16,8 +16,10 @@ The reference ships the three GEMMs of an MoE layer's expert projection
 
 Every operand is quantized by ``to_mx_both``, which reads the bf16 tensor once
 and writes both the row-wise and the transposed column-wise MX layouts, with
-the scales step-major (``scale_layout="steps"``): the layout the GEMM kernels
-read, so none of the three GEMMs re-lays scales per call.  The forward keeps
+the scales step-major (``scale_layout="steps"``) and the data in row pairs
+(``data_layout="pairs"``): the layouts the GEMM kernels read fastest, so none
+of the three GEMMs re-lays scales per call and every operand copy moves whole
+128-byte lines.  The forward keeps
 only the e4m3 layouts the backward needs (x^T along M and w^T along N, with
 their scales): half the bytes of keeping x and w in bf16.
 
@@ -40,11 +42,16 @@ from .forward import triton_mxfp8_grouped_mm
 from .quant import to_mx_both
 
 
+# quantizer output layouts of every operand (M, N, K multiples of 32: even
+# row counts, as row pairs need)
+_LAYOUTS = {"scale_layout": "steps", "data_layout": "pairs"}
+
+
 class _MXFP8GroupedMM(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, offs, out_dtype):
-        (sx, qx), (sxt, qxt) = to_mx_both(x, scale_layout="steps")   # (M, K) along K; (K, M) along M
-        (sw, qw), (swt, qwt) = to_mx_both(w, scale_layout="steps")   # (E, N, K) along K; (E, K, N) along N
+        (sx, qx), (sxt, qxt) = to_mx_both(x, **_LAYOUTS)   # (M, K) along K; (K, M) along M
+        (sw, qw), (swt, qwt) = to_mx_both(w, **_LAYOUTS)   # (E, N, K) along K; (E, K, N) along N
         out = triton_mxfp8_grouped_mm(qx, qw, sx, sw, offs, out_dtype=out_dtype)
         ctx.save_for_backward(qxt, sxt, qwt, swt, offs)
         ctx.x_dtype = x.dtype
@@ -54,7 +61,7 @@ class _MXFP8GroupedMM(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         qxt, sxt, qwt, swt, offs = ctx.saved_tensors
-        (sg, qg), (sgt, qgt) = to_mx_both(grad_out.contiguous(), scale_layout="steps")   # along N; (N, M) along M
+        (sg, qg), (sgt, qgt) = to_mx_both(grad_out.contiguous(), **_LAYOUTS)   # along N; (N, M) along M
         grad_x = grad_w = None
         if ctx.needs_input_grad[0]:
             grad_x = triton_mxfp8_grouped_mm(qg, qwt, sg, swt, offs, out_dtype=ctx.x_dtype)

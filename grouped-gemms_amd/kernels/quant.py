@@ -17,6 +17,15 @@ kernels/forward.py:367-397, is redone on every call): an int32 tensor
 ``128t .. 128t+127`` of row r (byte j: block 4t+j; bytes past the row 127).
 ``triton_mxfp8_grouped_mm`` / ``triton_mxfp8_wgrad`` recognise such int32
 scales and skip their per-call re-layout.
+
+``data_layout="pairs"`` makes them write the e4m3 data in row pairs: rows 2i
+and 2i+1 interleaved in 64-byte pieces, returned as the strided view
+``(*batch, R/2, 2, cdiv(L, 64), 64)`` (``_common._pair_buffer``; the pad
+bytes past L are zero).  The GEMMs stage a 64-element slice of two adjacent
+rows per step, which is then one 128-byte line instead of halves of two:
+13% less time for the forward and 20% for the weight gradient over the
+benchmark shapes, same bits.  The GEMM wrappers recognise such views (with
+step-major scales).
 """
 
 from __future__ import annotations
@@ -24,7 +33,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._common import _require, _stream_handle
+from ._common import _pair_buffer, _require, _stream_handle
 
 _SRC_CODES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16,
               torch.float32: _lib.DTYPE_F32}
@@ -43,6 +52,14 @@ def _layout_code(scale_layout: str) -> int:
     if scale_layout == "steps":
         return _lib.SCALES_STEPS
     raise ValueError(f"scale_layout must be 'plain' or 'steps', got {scale_layout!r}")
+
+
+def _pairs_flag(data_layout: str) -> bool:
+    if data_layout == "rows":
+        return False
+    if data_layout == "pairs":
+        return True
+    raise ValueError(f"data_layout must be 'rows' or 'pairs', got {data_layout!r}")
 
 
 def _aligned_rows(batch: tuple, rows: int, length: int, device) -> tuple:
@@ -65,7 +82,7 @@ def step_scales_shape(batch: tuple, rows: int, length: int) -> tuple:
 
 
 def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32, *,
-          scale_layout: str = "plain"):
+          scale_layout: str = "plain", data_layout: str = "rows"):
     """Quantize ``data`` along its last dim; returns ``(scales_u8, data_q)``.
 
     ``elem_dtype`` float8_e4m3fn gives ``data_q`` of ``data``'s shape;
@@ -74,6 +91,8 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
     by 32.  Asserts like the reference (utils.py:78-81).  With
     ``scale_layout="steps"`` the scales are step-major int32
     ``(*data.shape[:-2], cdiv(L, 128), data.shape[-2])`` instead.
+    ``data_layout="pairs"`` (e4m3, ``data.shape[-2]`` even): ``data_q`` in
+    row pairs, the view ``(*data.shape[:-2], R/2, 2, cdiv(L, 64), 64)``.
     """
     fp4 = _FP4 is not None and elem_dtype is _FP4
     assert elem_dtype is torch.float8_e4m3fn or fp4, "only e4m3fn and e2m1fn_x2 supported"
@@ -91,7 +110,15 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
     rows = x.shape[0]
     qcols = L // 2 if fp4 else L
     lay = _layout_code(scale_layout)
-    q = torch.empty((rows, qcols), dtype=torch.uint8, device=data.device)
+    pairs = _pairs_flag(data_layout)
+    if pairs:
+        if fp4 or len(shape) < 2:
+            raise ValueError("data_layout='pairs' needs e4m3 output and at least 2 dims")
+        qv, ld_q = _pair_buffer(shape[:-2], shape[-2], L, data.device)
+        q_ptr = qv.data_ptr()
+    else:
+        q = torch.empty((rows, qcols), dtype=torch.uint8, device=data.device)
+        q_ptr, ld_q = q.data_ptr(), qcols
     if lay == _lib.SCALES_STEPS:
         R = shape[-2] if len(shape) >= 2 else 1
         s = torch.empty(step_scales_shape(shape[:-2], R, L), dtype=torch.int32, device=data.device)
@@ -102,24 +129,28 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
     lib = _lib.load()
     rc = lib.mxgg_quantize_mx(x.data_ptr(), code, rows, L, x.stride(0) if rows > 1 else L,
                               _lib.FMT_E2M1 if fp4 else _lib.FMT_E4M3,
-                              q.data_ptr(), qcols, s.data_ptr(), ld_s, lay,
+                              q_ptr, ld_q, s.data_ptr(), ld_s, lay | (_lib.DATA_PAIRS if pairs else 0),
                               _stream_handle(data.device))
     _lib.check(rc)
-    q = q.view(_FP4 if fp4 else torch.float8_e4m3fn).reshape(shape[:-1] + (qcols,))
+    if pairs:
+        q = qv.view(torch.float8_e4m3fn)
+    else:
+        q = q.view(_FP4 if fp4 else torch.float8_e4m3fn).reshape(shape[:-1] + (qcols,))
     if lay == _lib.SCALES_STEPS:
         return s, q
     return s.reshape(shape[:-1] + (L // 32,)), q
 
 
 def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32, *,
-               scale_layout: str = "plain"):
+               scale_layout: str = "plain", data_layout: str = "rows"):
     """``to_mx(data.t().contiguous())`` for a 2-D ``(R, C)`` tensor in one pass.
 
     Returns ``(scales (C, R//32) uint8, data (C, R) float8_e4m3fn)``; with
     ``scale_layout="steps"`` the scales are step-major int32
     ``(cdiv(R, 128), C)``.  When R is not a multiple of 128 the data is a
     view whose row stride is R rounded up to 128 (same values, rows on the
-    128-byte grid for the weight-gradient GEMM).
+    128-byte grid for the weight-gradient GEMM).  ``data_layout="pairs"``:
+    the data in row pairs, the view ``(C/2, 2, cdiv(R, 64), 64)``.
     """
     assert elem_dtype is torch.float8_e4m3fn, "to_mx_dim0 supports e4m3fn only"
     assert block_size == 32, "block_size must be 32 (OCP MX)"
@@ -135,7 +166,8 @@ def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
     if (C * x.element_size()) % 16:
         raise ValueError(f"to_mx_dim0 needs dim 1 ({C}) to span a multiple of 16 bytes")
     lay = _layout_code(scale_layout)
-    q, ld_q = _aligned_rows((), C, R, data.device)
+    pairs = _pairs_flag(data_layout)
+    q, ld_q = (_pair_buffer if pairs else _aligned_rows)((), C, R, data.device)
     if lay == _lib.SCALES_STEPS:
         s = torch.empty(step_scales_shape((), C, R), dtype=torch.int32, device=data.device)
         ld_s = C
@@ -144,14 +176,14 @@ def to_mx_dim0(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
         ld_s = R // 32
     lib = _lib.load()
     rc = lib.mxgg_quantize_mx_dim0(x.data_ptr(), code, R, C, x.stride(0), _lib.FMT_E4M3,
-                                   q.data_ptr(), ld_q, s.data_ptr(), ld_s, lay,
+                                   q.data_ptr(), ld_q, s.data_ptr(), ld_s, lay | (_lib.DATA_PAIRS if pairs else 0),
                                    _stream_handle(data.device))
     _lib.check(rc)
     return s, q.view(torch.float8_e4m3fn)
 
 
 def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 32, *,
-               scale_layout: str = "plain"):
+               scale_layout: str = "plain", data_layout: str = "rows"):
     """``(to_mx(data), to_mx(data.transpose(-2, -1).contiguous()))`` in one pass.
 
     ``data`` is ``(R, C)`` or ``(B, R, C)`` with ``R`` and ``C`` multiples of
@@ -161,6 +193,8 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
     ``(.., cdiv(C, 128), R)`` and ``(.., cdiv(R, 128), C)``.  Either data
     output whose row length (C, resp. R) is not a multiple of 128 is a view
     with the row stride rounded up to 128 (as in ``to_mx_dim0``).
+    ``data_layout="pairs"``: both data outputs in row pairs, the views
+    ``(.., R/2, 2, cdiv(C, 64), 64)`` and ``(.., C/2, 2, cdiv(R, 64), 64)``.
     """
     assert elem_dtype is torch.float8_e4m3fn, "to_mx_both supports e4m3fn only"
     assert block_size == 32, "block_size must be 32 (OCP MX)"
@@ -176,8 +210,10 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
         raise ValueError(f"to_mx_both needs the last dim ({C}) to span a multiple of 16 bytes")
     dev = data.device
     lay = _layout_code(scale_layout)
-    q_r, ld_qr = _aligned_rows((B,), R, C, dev)
-    q_c, ld_qc = _aligned_rows((B,), C, R, dev)
+    pairs = _pairs_flag(data_layout)
+    out = _pair_buffer if pairs else _aligned_rows
+    q_r, ld_qr = out((B,), R, C, dev)
+    q_c, ld_qc = out((B,), C, R, dev)
     if lay == _lib.SCALES_STEPS:
         s_r = torch.empty(step_scales_shape((B,), R, C), dtype=torch.int32, device=dev)
         s_c = torch.empty(step_scales_shape((B,), C, R), dtype=torch.int32, device=dev)
@@ -188,7 +224,8 @@ def to_mx_both(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: i
         ld_r, ld_c = C // 32, R // 32
     lib = _lib.load()
     rc = lib.mxgg_quantize_mx_both(x.data_ptr(), code, B, R, C, C, q_r.data_ptr(), ld_qr, s_r.data_ptr(), ld_r,
-                                   q_c.data_ptr(), ld_qc, s_c.data_ptr(), ld_c, lay, _stream_handle(dev))
+                                   q_c.data_ptr(), ld_qc, s_c.data_ptr(), ld_c,
+                                   lay | (_lib.DATA_PAIRS if pairs else 0), _stream_handle(dev))
     _lib.check(rc)
     q_r, q_c = q_r.view(torch.float8_e4m3fn), q_c.view(torch.float8_e4m3fn)
     if data.dim() == 2:

@@ -30,6 +30,17 @@
  * request, and the *_steps GEMM entry points take it, skipping the per-call
  * re-layout of plain scales.  (Not the reference's CDNA4 pre-shuffle,
  * kernels/forward.py:367-397: one 128-element step of a row is one dword.)
+ *
+ * Row-pair data (MXGG_DATA_PAIRS for the quantizers, MXGG_A_PAIRS /
+ * MXGG_B_PAIRS for the *_steps GEMMs; no counterpart in the reference, whose
+ * operands are row-major): an e4m3 operand of R rows (R even) whose rows hold
+ * L bytes, with "row stride" ld >= L rounded up to 64, keeps byte k of row r
+ * at (r/2)*2*ld + (k/64)*128 + (r%2)*64 + k%64.  The 64-byte pieces of rows 2i
+ * and 2i+1 alternate, so the 64-element slice of two adjacent rows that the
+ * GEMM stages per step is one 128-byte line (row-major, each is half of two
+ * lines).  Bytes L .. L rounded up to 64 of a row are padding, which the
+ * GEMMs do not read (they take the true K, resp. M); the quantizers write
+ * zeros there.
  */
 #ifndef MXGG_H_
 #define MXGG_H_
@@ -41,7 +52,7 @@
 extern "C" {
 #endif
 
-#define MXGG_VERSION 3000 /* major*1000 + minor */
+#define MXGG_VERSION 4000 /* major*1000 + minor */
 
 /* status codes */
 #define MXGG_OK 0
@@ -59,9 +70,16 @@ extern "C" {
 #define MXGG_DTYPE_F16 1
 #define MXGG_DTYPE_F32 2
 
-/* scale layouts of the quantizer outputs */
+/* scale layouts of the quantizer outputs, and the data-layout flag OR-ed
+ * into the same argument */
 #define MXGG_SCALES_PLAIN 0   /* (rows, nblk) bytes, row stride ld_s */
 #define MXGG_SCALES_STEPS 1   /* step-major dwords (see above); ld_s = R, the rows per batch */
+#define MXGG_DATA_PAIRS 2     /* e4m3 data outputs in row pairs (see above) */
+
+/* operand layouts of mxgg_grouped_mm_steps / mxgg_wgrad_steps (bit flags;
+ * 0 = both row-major) */
+#define MXGG_A_PAIRS 1   /* A (forward) or go_t (wgrad) in row pairs */
+#define MXGG_B_PAIRS 2   /* B (forward; e4m3 only) or ia_t (wgrad) in row pairs */
 
 /* Library version (MXGG_VERSION of the build). */
 int mxgg_version(void);
@@ -84,6 +102,8 @@ int mxgg_device_supported(void);
  *              ld_s.  MXGG_SCALES_STEPS: step-major for batches of ld_s rows
  *              (ld_s divides rows; e.g. ld_s = N for an (E, N, K) weight
  *              given as E*N rows), 4 * rows * ceil(cols/128) bytes.
+ *   scale_layout | MXGG_DATA_PAIRS: q in row pairs (E4M3, rows even, ld_q a
+ *              multiple of 64 and at least cols rounded up to 64).
  * cols must be a multiple of 32.
  */
 int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
@@ -98,6 +118,8 @@ int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
  *   q       (cols, rows) e4m3 bytes, row stride ld_q (elem_fmt must be E4M3)
  *   scales  MXGG_SCALES_PLAIN: (cols, rows/32) bytes, row stride ld_s;
  *           MXGG_SCALES_STEPS: step-major [ceil(rows/128)][cols] dwords (ld_s = cols)
+ *   scale_layout | MXGG_DATA_PAIRS: q in row pairs (cols even, ld_q a multiple
+ *           of 64 and at least rows rounded up to 64)
  */
 int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t cols,
                           int64_t ld_src, int elem_fmt, void* q, int64_t ld_q,
@@ -118,6 +140,8 @@ int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t rows, int64_t 
  *   q_cols  (batch, cols, rows) e4m3, row stride ld_qc;  s_cols (batch, cols, rows/32), row stride ld_sc
  *   scale_layout MXGG_SCALES_STEPS: s_rows is [batch][ceil(cols/128)][rows] and s_cols
  *           [batch][ceil(rows/128)][cols] dwords (ld_sr = rows, ld_sc = cols)
+ *   scale_layout | MXGG_DATA_PAIRS: q_rows and q_cols in row pairs (ld_qr, ld_qc
+ *           multiples of 64, at least cols, resp. rows, rounded up to 64)
  */
 int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t batch, int64_t rows, int64_t cols,
                           int64_t ld_src, void* q_rows, int64_t ld_qr, uint8_t* s_rows, int64_t ld_sr,
@@ -209,16 +233,19 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
  * quantizers): A_ss [T][M] and B_ss [E][T][N] uint32, T = ceil(K/128).  The
  * same GEMM launches without the per-call re-layout of plain scales (the
  * reference pre-shuffles its scales on every call too, kernels/forward.py:
- * 367-397, 528-550).  workspace / ws_bytes (may be null / 0): room for the
- * fp32 partial tiles of a split last round; mxgg_grouped_mm_workspace_size()
- * is always enough.  Results are bit-identical to mxgg_grouped_mm given a
- * workspace with the same room after its scales.
+ * 367-397, 528-550).  layout: MXGG_A_PAIRS and / or MXGG_B_PAIRS for operands
+ * in row pairs (lda, ldb_n then at least K rounded up to 64; M, resp. N,
+ * even).  workspace / ws_bytes (may be null / 0): room for
+ * the fp32 partial tiles of a split last round;
+ * mxgg_grouped_mm_workspace_size() is always enough.  Results are
+ * bit-identical to mxgg_grouped_mm given a workspace with the same room after
+ * its scales, in either operand layout.
  */
 int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32_t* A_ss,
                           const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint32_t* B_ss,
                           const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
                           void* out, int out_dtype, int64_t ldo,
-                          int block_m, int block_n, int group_m, int xcd_swizzle,
+                          int block_m, int block_n, int group_m, int xcd_swizzle, int layout,
                           void* workspace, size_t ws_bytes, void* stream);
 
 /*
@@ -272,14 +299,18 @@ int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t 
 /*
  * mxgg_wgrad with step-major scales: go_ss [T][N] and ia_ss [T][K] uint32,
  * T = ceil(M/128) (mxgg_quantize_mx_dim0 / _both with MXGG_SCALES_STEPS), no
- * re-layout.  workspace / ws_bytes (may be null / 0): room for the fp32
+ * re-layout.  layout: MXGG_A_PAIRS (go_t) and / or MXGG_B_PAIRS (ia_t) for
+ * operands in row pairs (ld_go, ld_ia then at least M rounded up to 64; N,
+ * resp. K, even).  workspace / ws_bytes (may be null / 0): room for the fp32
  * partial tiles of tiles cut along the tokens; mxgg_wgrad_workspace_size() is
- * always enough.  Bit-identical to mxgg_wgrad given the same room.
+ * always enough.  Bit-identical to mxgg_wgrad given the same room, in either
+ * operand layout.
  */
 int mxgg_wgrad_steps(const uint8_t* go_t, int64_t ld_go, const uint32_t* go_ss,
                      const uint8_t* ia_t, int64_t ld_ia, const uint32_t* ia_ss,
                      const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,
-                     void* out, int out_dtype, void* workspace, size_t ws_bytes, void* stream);
+                     void* out, int out_dtype, int layout, void* workspace, size_t ws_bytes,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.mxgg_version() == 3000
+    assert lib.mxgg_version() == 4000
     assert isinstance(lib.mxgg_last_error_string(), bytes)
 
 
@@ -153,15 +153,57 @@ def test_wgrad_and_quant_validation_without_gpu():
     rc = lib.mxgg_quantize_mx(16, 0, 6, 64, 64, 0, 16, 64, 16, 4, _lib.SCALES_STEPS, None)
     assert rc == _lib.ERR_INVALID_ARG and b"rows per batch" in lib.mxgg_last_error_string()
     rc = lib.mxgg_quantize_mx(16, 0, 6, 64, 64, 0, 16, 64, 16, 2, 9, None)
-    assert rc == _lib.ERR_INVALID_ARG and b"scale_layout" in lib.mxgg_last_error_string()
+    assert rc == _lib.ERR_INVALID_ARG and b"layout 9" in lib.mxgg_last_error_string()
     rc = lib.mxgg_quantize_mx_dim0(16, 0, 64, 96, 96, 0, 16, 64, 16, 64, _lib.SCALES_STEPS, None)
     assert rc == _lib.ERR_INVALID_ARG
     # GEMMs on step-major scales: scale words must be 4-byte aligned; wgrad still needs M % 32 == 0
     rc = lib.mxgg_grouped_mm_steps(16, 64, 18, 16, 0, 64, 64 * 64, 16, 16, 1, 64, 64, 64,
-                                   16, 0, 64, 0, 0, 0, 0, None, 0, None)
+                                   16, 0, 64, 0, 0, 0, 0, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"aligned" in lib.mxgg_last_error_string()
-    rc = lib.mxgg_wgrad_steps(16, 48, 16, 16, 48, 16, 16, 1, 48, 8, 8, 16, 0, None, 0, None)
+    rc = lib.mxgg_wgrad_steps(16, 48, 16, 16, 48, 16, 16, 1, 48, 8, 8, 16, 0, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"multiple of 32" in lib.mxgg_last_error_string()
+
+
+def test_row_pair_argument_checks():
+    """Row-pair operands (MXGG_DATA_PAIRS / MXGG_A_PAIRS / MXGG_B_PAIRS) are
+    checked before anything launches: even row counts, strides that hold
+    the rows rounded up to 64 bytes, e4m3 only, known flags."""
+    from kernels import _lib
+    lib = _lib.load()
+    P, S = _lib.DATA_PAIRS, _lib.SCALES_STEPS
+    err = lib.mxgg_last_error_string
+    # quantizers: rows must pair up; the stride a multiple of 64 holding the padded row; e4m3 only
+    rc = lib.mxgg_quantize_mx(16, 0, 5, 64, 64, 0, 16, 64, 16, 2, P, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    rc = lib.mxgg_quantize_mx(16, 0, 6, 96, 96, 0, 16, 112, 16, 3, P, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 64" in err()
+    rc = lib.mxgg_quantize_mx(16, 0, 6, 96, 96, 0, 16, 96, 16, 3, P, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 64 and holds 128 bytes" in err()
+    rc = lib.mxgg_quantize_mx(16, 0, 6, 64, 64, _lib.FMT_E2M1, 16, 64, 16, 2, P, None)
+    assert rc == _lib.ERR_UNSUPPORTED
+    assert lib.mxgg_quantize_mx(16, 0, 6, 96, 96, 0, 16, 128, 16, 6, P | S, None) != _lib.ERR_INVALID_ARG
+    rc = lib.mxgg_quantize_mx_dim0(16, 0, 96, 64, 64, 0, 16, 96, 16, 64, P | S, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 64" in err()
+    rc = lib.mxgg_quantize_mx_both(16, 0, 1, 96, 64, 64, 16, 64, 16, 96, 16, 112, 16, 64, P | S, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 64" in err()
+    # forward: known flags; e4m3 weights only; M / N even; strides hold K rounded up to 64
+    fwd = lambda M, N, K, lda, ldb, fmt, layout: lib.mxgg_grouped_mm_steps(
+        16, lda, 16, 16, fmt, ldb, N * ldb, 16, 16, 1, M, N, K, 16, 0, N, 0, 0, 0, 0, layout, None, 0, None)
+    assert fwd(64, 64, 64, 64, 64, 0, 4) == _lib.ERR_INVALID_ARG and b"layout flags" in err()
+    assert fwd(64, 64, 64, 64, 32, _lib.FMT_E2M1, _lib.B_PAIRS) == _lib.ERR_UNSUPPORTED
+    assert fwd(63, 64, 64, 64, 64, 0, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert fwd(64, 65, 64, 64, 64, 0, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert fwd(63, 65, 64, 64, 64, 0, 0) != _lib.ERR_INVALID_ARG       # odd counts are fine row-major
+    assert fwd(64, 64, 96, 112, 128, 0, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
+    assert fwd(64, 64, 96, 128, 112, 0, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
+    # wgrad: the same for go_t (A_PAIRS) and ia_t (B_PAIRS) along the tokens
+    wg = lambda M, N, K, ldg, ldi, layout: lib.mxgg_wgrad_steps(
+        16, ldg, 16, 16, ldi, 16, 16, 1, M, N, K, 16, 0, layout, None, 0, None)
+    assert wg(96, 64, 64, 128, 128, 8) == _lib.ERR_INVALID_ARG and b"layout flags" in err()
+    assert wg(96, 63, 64, 128, 128, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert wg(96, 64, 65, 128, 128, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert wg(96, 64, 64, 112, 128, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
+    assert wg(96, 64, 64, 128, 112, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
 
 
 def test_import_surface_matches_reference():
@@ -203,7 +245,7 @@ def test_to_mx_signature_matches_reference():
     assert pos == ["data", "elem_dtype", "block_size"]
     assert sig.parameters["block_size"].default == 32
     extra = [p for p in sig.parameters.values() if p.kind == p.KEYWORD_ONLY]
-    assert [p.name for p in extra] == ["scale_layout"] and extra[0].default == "plain"
+    assert [(p.name, p.default) for p in extra] == [("scale_layout", "plain"), ("data_layout", "rows")]
 
 
 def test_cpu_tensors_fail_loudly():

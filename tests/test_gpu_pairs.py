@@ -1,0 +1,249 @@
+"""Row-pair operands (``data_layout="pairs"`` / ``MXGG_DATA_PAIRS``,
+``MXGG_A_PAIRS`` / ``MXGG_B_PAIRS``): rows 2i and 2i+1 interleaved in 64-byte
+pieces, so the GEMMs copy whole 128-byte lines.  A layout of this build with
+no counterpart in the reference, held to the row-major path bit for bit:
+
+* the quantizers' row-pair output holds the bytes of their row-major output
+  (read back through the returned view, and at the byte offsets the C header
+  documents, on the raw storage), the pad past an odd multiple of 32 is
+  zero, and the scales are unchanged;
+* ``to_row_pairs`` of row-major data equals the quantizers' row-pair output;
+* the forward / dgrad and wgrad GEMMs return the same bits with either
+  operand, or both, in row pairs as with both row-major: group starts at odd
+  rows (a tile whose first row is the second of a pair), partial tiles,
+  128 x 128 tiles, split launches and (among the benchmark shapes)
+  quarter-tile ones, f32 / f16 outputs, an e2m1 weight beside a row-pair A,
+  token ranges off the 16 grid (the wgrad's edge chunks), 2080 tokens (rows
+  padded to 2112), and every benchmark shape.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mx_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+M_TOKENS = 16640
+SHAPES = [(e, n, k) for e in (1, 2, 4, 8) for n in (2048, 5120, 8192) for k in (2048, 5120, 8192)]
+
+
+def _x(shape, seed, dev, std=1.0, dtype=torch.bfloat16):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=dev) * std).to(dtype)
+
+
+def _u8(t):
+    return t.view(torch.uint8)
+
+
+def _rows_of(pairs, L):
+    """Row-major bytes (.., R, L) and the pad (.., R, Lp - L) of a row-pair view."""
+    *b, P, two, S, w = pairs.shape
+    r = _u8(pairs).reshape(tuple(b) + (2 * P, 64 * S))
+    return r[..., :L], r[..., L:]
+
+
+def _odd_offs(E, M, seed):
+    """Cumulative group ends with odd starts and bounds off the 16 grid."""
+    rng = np.random.default_rng(seed)
+    cuts = np.sort(rng.choice(np.arange(1, M), size=E - 1, replace=False)) if E > 1 else np.array([], dtype=np.int64)
+    cuts = [c | 1 for c in cuts]                     # odd: the next group starts on the second row of a pair
+    return np.array(sorted(cuts) + [M], dtype=np.int32)
+
+
+# ---------------------------------------------------------------------------
+# quantizers
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(96, 544), (3, 40, 96), (8, 128), (2080, 96)])
+def test_to_mx_pairs_holds_the_rows(gpu, dtype, shape):
+    import kernels
+    from kernels._common import to_row_pairs
+    x = _x(shape, sum(shape), gpu, 3.0, dtype)
+    s_r, q_r = kernels.to_mx(x, scale_layout="steps")
+    s_p, q_p = kernels.to_mx(x, scale_layout="steps", data_layout="pairs")
+    L = shape[-1]
+    assert q_p.dtype == torch.float8_e4m3fn
+    assert tuple(q_p.shape) == shape[:-2] + (shape[-2] // 2, 2, -(-L // 64), 64)
+    assert torch.equal(s_p, s_r)
+    rows, pad = _rows_of(q_p, L)
+    assert torch.equal(rows, _u8(q_r))
+    assert not pad.any()
+    assert torch.equal(_u8(to_row_pairs(q_r)).reshape(rows.shape[:-1] + (-1,)),
+                       _u8(q_p).reshape(rows.shape[:-1] + (-1,)))
+
+
+def test_pair_storage_matches_documented_offsets(gpu):
+    """Byte k of row r at (r/2) 2 ld + (k/64) 128 + (r%2) 64 + k%64 of the
+    storage (the formula of include/mxgg.h), pad bytes zero."""
+    import kernels
+    R, L = 6, 96
+    x = _x((R, L), 5, gpu, 2.0)
+    _, q_r = kernels.to_mx(x)
+    _, q_p = kernels.to_mx(x, data_layout="pairs")
+    ld = 128
+    flat = torch.as_strided(_u8(q_p), (R // 2 * 2 * ld,), (1,)).cpu().numpy()
+    rows = _u8(q_r).cpu().numpy()
+    r, k = np.meshgrid(np.arange(R), np.arange(ld), indexing="ij")
+    at = (r // 2) * 2 * ld + (k // 64) * 128 + (r % 2) * 64 + k % 64
+    np.testing.assert_array_equal(flat[at[:, :L]], rows)
+    assert not flat[at[:, L:]].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(2080, 256), (96, 544), (2, 160, 96), (64, 32)])
+def test_to_mx_both_and_dim0_pairs_hold_the_rows(gpu, dtype, shape):
+    import kernels
+    x = _x(shape, sum(shape) + 7, gpu, 3.0, dtype)
+    (s_r, q_r), (s_c, q_c) = kernels.to_mx_both(x, scale_layout="steps")
+    (t_r, p_r), (t_c, p_c) = kernels.to_mx_both(x, scale_layout="steps", data_layout="pairs")
+    R, C = shape[-2:]
+    assert torch.equal(t_r, s_r) and torch.equal(t_c, s_c)
+    for q, p, L in ((q_r, p_r, C), (q_c, p_c, R)):
+        rows, pad = _rows_of(p, L)
+        assert torch.equal(rows, _u8(q))
+        assert not pad.any()
+    if x.dim() == 2:
+        s_d, q_d = kernels.to_mx_dim0(x, scale_layout="steps", data_layout="pairs")
+        assert torch.equal(s_d, s_c)
+        rows, pad = _rows_of(q_d, R)
+        assert torch.equal(rows, _u8(q_c)) and not pad.any()
+
+
+def test_pairs_need_e4m3_and_even_rows(gpu):
+    import kernels
+    with pytest.raises(ValueError):
+        kernels.to_mx(_x((3, 64), 1, gpu), data_layout="pairs")
+    with pytest.raises(ValueError):
+        kernels.to_mx(_x((4, 64), 1, gpu), elem_dtype=torch.float4_e2m1fn_x2, data_layout="pairs")
+    with pytest.raises(ValueError):
+        kernels.to_mx(_x((4, 64), 1, gpu), data_layout="cols")
+
+
+# ---------------------------------------------------------------------------
+# forward / dgrad
+# ---------------------------------------------------------------------------
+
+def _fwd_all_layouts(gpu, E, M, N, K, offs, seed, out_dtype=torch.bfloat16, fp4=False):
+    """Forward with A / B row-major and in row pairs: every layout's valid
+    rows equal the row-major call's bit for bit."""
+    import kernels
+    from kernels._common import to_row_pairs
+    a = _x((M, K), seed, gpu)
+    w = _x((E, N, K), seed + 1, gpu, 0.05)
+    sa, qa = kernels.to_mx(a, scale_layout="steps")
+    fp = torch.float4_e2m1fn_x2 if fp4 else torch.float8_e4m3fn
+    sw, qw = kernels.to_mx(w, elem_dtype=fp, scale_layout="steps")
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    rows = int(offs[-1])
+    ref = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, o, out_dtype=out_dtype)[:rows]
+    pa = to_row_pairs(qa)
+    cases = {"A pairs": (pa, qw)}
+    if not fp4:
+        pw = to_row_pairs(qw)
+        cases.update({"B pairs": (qa, pw), "both": (pa, pw)})
+    for what, (x_, w_) in cases.items():
+        got = kernels.triton_mxfp8_grouped_mm(x_, w_, sa, sw, o, out_dtype=out_dtype)[:rows]
+        assert torch.equal(got.view(torch.uint8), ref.view(torch.uint8)), f"{what}: E={E} M={M} N={N} K={K}"
+    return ref
+
+
+@pytest.mark.parametrize("case", [
+    (4, 4096, 512, 1024, "odd"),          # odd group starts: shifted pairs
+    (2, 512, 256, 512, "odd"),            # small problem: 128 x 128 tiles
+    (1, 512, 512, 8192, "even"),          # a lone round split along K
+    (3, 1000, 320, 1056, "odd"),          # K % 64 == 32, partial row and column tiles
+    (1, 2080, 2048, 2048, "even"),        # one GPU's share under 8-way expert parallelism
+    (16, 16640, 256, 2048, "odd"),        # many groups, 256-wide N
+], ids=lambda c: "E{}_M{}_N{}_K{}_{}".format(*c))
+def test_fwd_pairs_bitwise(gpu, case):
+    import random
+    E, M, N, K, kind = case
+    offs = _odd_offs(E, M, E + M) if kind == "odd" else O.generate_jagged_offs(E, M, 32, rng=random.Random(E * 7 + N))
+    _fwd_all_layouts(gpu, E, M, N, K, offs, seed=M + K)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_fwd_pairs_other_outputs(gpu, out_dtype):
+    _fwd_all_layouts(gpu, 3, 1536, 384, 768, _odd_offs(3, 1536, 9), seed=4, out_dtype=out_dtype)
+
+
+def test_fwd_pairs_beside_e2m1_weight(gpu):
+    _fwd_all_layouts(gpu, 4, 2048, 512, 1024, _odd_offs(4, 2048, 3), seed=11, fp4=True)
+
+
+def test_fwd_pairs_need_step_scales(gpu):
+    import kernels
+    from kernels._common import to_row_pairs
+    a = _x((64, 128), 1, gpu)
+    w = _x((2, 64, 128), 2, gpu)
+    sa, qa = kernels.to_mx(a)
+    sw, qw = kernels.to_mx(w)
+    o = torch.tensor([32, 64], dtype=torch.int32, device=gpu)
+    with pytest.raises(TypeError):
+        kernels.triton_mxfp8_grouped_mm(to_row_pairs(qa), qw, sa, sw, o)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "E{}_N{}_K{}".format(*s))
+def test_sweep_fwd_pairs(gpu, shape):
+    """Every benchmark forward shape at 16640 tokens: both operands in row
+    pairs give the row-major bits."""
+    import random
+    E, N, K = shape
+    offs = O.generate_jagged_offs(E, M_TOKENS, 32, rng=random.Random(E * 131 + N + K))
+    _fwd_all_layouts(gpu, E, M_TOKENS, N, K, offs, seed=E + N + K)
+
+
+# ---------------------------------------------------------------------------
+# wgrad
+# ---------------------------------------------------------------------------
+
+def _wgrad_all_layouts(gpu, E, M, N, K, offs, seed, out_dtype=torch.bfloat16, quantizer_pairs=False):
+    import kernels
+    from kernels._common import to_row_pairs
+    go = _x((M, N), seed, gpu, 0.5)
+    ia = _x((M, K), seed + 1, gpu)
+    sg, qg = kernels.to_mx_dim0(go, scale_layout="steps")      # (N, M) along M
+    si, qi = kernels.to_mx_dim0(ia, scale_layout="steps")      # (K, M) along M
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    ref = kernels.triton_mxfp8_wgrad(qg, sg, qi, si, o, out_dtype=out_dtype)
+    if quantizer_pairs:
+        _, pg = kernels.to_mx_dim0(go, scale_layout="steps", data_layout="pairs")
+        _, pi = kernels.to_mx_dim0(ia, scale_layout="steps", data_layout="pairs")
+    else:
+        pg, pi = to_row_pairs(qg), to_row_pairs(qi)
+    for what, (g_, i_) in {"go pairs": (pg, qi), "ia pairs": (qg, pi), "both": (pg, pi)}.items():
+        got = kernels.triton_mxfp8_wgrad(g_, sg, i_, si, o, out_dtype=out_dtype)
+        assert torch.equal(got.view(torch.uint8), ref.view(torch.uint8)), f"{what}: E={E} M={M} N={N} K={K}"
+    return ref
+
+
+@pytest.mark.parametrize("case", [
+    (4, 2080, 512, 768, "odd"),           # 2080 tokens (rows padded to 2112), bounds off the 16 grid
+    (1, 16384, 256, 256, "even"),         # E = 1, few tiles: cut along the tokens
+    (3, 1056, 320, 192, "odd"),           # partial tiles in N and K
+    (80, 38048, 256, 256, "even"),        # more groups than the wave holds: device-planned split
+    (1, 2080, 2048, 2048, "even"),        # one GPU's share under 8-way expert parallelism
+], ids=lambda c: "E{}_M{}_N{}_K{}_{}".format(*c))
+def test_wgrad_pairs_bitwise(gpu, case):
+    import random
+    E, M, N, K, kind = case
+    offs = _odd_offs(E, M, E + N) if kind == "odd" else O.generate_jagged_offs(E, M, 32, rng=random.Random(E + M))
+    _wgrad_all_layouts(gpu, E, M, N, K, offs, seed=N + K)
+
+
+def test_wgrad_pairs_from_the_quantizer_f32(gpu):
+    _wgrad_all_layouts(gpu, 5, 2080, 384, 256, _odd_offs(5, 2080, 1), seed=3, out_dtype=torch.float32,
+                       quantizer_pairs=True)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "E{}_N{}_K{}".format(*s))
+def test_sweep_wgrad_pairs(gpu, shape):
+    """Every benchmark wgrad shape at 16640 tokens, row pairs against row-major."""
+    import random
+    E, N, K = shape
+    offs = O.generate_jagged_offs(E, M_TOKENS, 32, rng=random.Random(E * 137 + N + K))
+    _wgrad_all_layouts(gpu, E, M_TOKENS, N, K, offs, seed=E * N + K)
