@@ -24,7 +24,11 @@ Beside it, each call is timed again on step-major scales (the layout the
 kernels read, so the call launches no re-layout): between its events lie
 only the GEMM launches of the call (the whole-tile kernel, and the piece /
 quarter-tile / reduce launches when its last round is split).  The roofline
-of the dominant kernel uses that time.  Also measured
+of the dominant kernel uses that time.  After the sweep, it runs once more on
+the operands' native layout (``kernels.quant``: step-major scales and row-pair
+data, ``data_layout="pairs"``, written by the quantizers outside the timed
+region): kernel-only time again, reported as ``native_geomean_tflops`` and
+``roofline_native`` beside the drop-in headline.  Also measured
 (e4m3 x e2m1, E=8, M=16640, N=8192, K=5120), the quantizer in GB/s, one
 training step (forward + backward) of the MoE layer (kernels/moe.py) and one
 GPU's share of the sweep under 8-way expert parallelism (E=1, M=2080).
@@ -135,8 +139,10 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
 
     Each counter is scaled so that the calibration copy (256 MiB each way)
     reads 256 MiB; dispatches are matched to sweep shapes by launch order
-    (per shape: fwd, dgrad, wgrad, each warmup + steps launches) to set the
-    algorithmic bytes beside the measured ones."""
+    (per shape: fwd, dgrad, wgrad, each call timed twice, warmup + steps
+    launches each; then the native-layout sweep, each call once) to set the
+    algorithmic bytes beside the measured ones.  Kernels of the native sweep
+    are listed with the suffix " [row pairs]"."""
     import csv
 
     def load(path, counter):
@@ -159,37 +165,40 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
         scaled[counter] = [(n, v * factor * 1024.0) for _, n, v in rows
                            if ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n]
     f, w = scaled["FETCH_SIZE"], scaled["WRITE_SIZE"]
-    # each call is timed twice (plain scales, then step-major), warmup + steps launches each
-    per = 2 * (warmup + steps)
+    # each call is timed twice (plain scales, then step-major), warmup + steps
+    # launches each; the native sweep times each call once
     shapes = SHAPES[:n_shapes]
     want = []
-    for (e, n, k) in shapes:
-        for kind in ("fwd", "dgrad", "wgrad"):
-            if kind == "wgrad":
-                alg = (n + k) * M_TOKENS * (1 + 1 / 32) + 2 * e * n * k
-            else:
-                nn, kk = (n, k) if kind == "fwd" else (k, n)
-                alg = M_TOKENS * kk * (1 + 1 / 32) + e * nn * kk * (1 + 1 / 32) + 2 * M_TOKENS * nn
-            want += [(kind, alg, (e, n, k))] * per
+    for tag, per in (("", 2 * (warmup + steps)), (NATIVE_TAG, warmup + steps)):
+        for (e, n, k) in shapes:
+            for kind in ("fwd", "dgrad", "wgrad"):
+                if kind == "wgrad":
+                    alg = (n + k) * M_TOKENS * (1 + 1 / 32) + 2 * e * n * k
+                else:
+                    nn, kk = (n, k) if kind == "fwd" else (k, n)
+                    alg = M_TOKENS * kk * (1 + 1 / 32) + e * nn * kk * (1 + 1 / 32) + 2 * M_TOKENS * nn
+                want += [(kind, alg, (e, n, k), tag)] * per
     if len(f) != len(w):
         raise SystemExit(f"dispatch count mismatch: fetch {len(f)}, write {len(w)}")
     # a wgrad call whose tiles are all split launches no whole-tile kernel:
     # its entry in `want` has no dispatch and is skipped
     matched = []
     i = 0
-    for kind, alg, shape in want:
+    for kind, alg, shape, tag in want:
+        if i >= len(f) and tag:
+            break                # a run without the native sweep (--no-native)
         if i < len(f) and (("wgrad" in f[i][0]) == (kind == "wgrad")):
-            matched.append((f[i], w[i], (kind, alg, shape)))
+            matched.append((f[i], w[i], (kind, alg, shape, tag)))
             i += 1
         elif kind != "wgrad":
             raise SystemExit(f"dispatch {i} ({f[i][0] if i < len(f) else 'none'}) does not match a {kind} call")
     if i != len(f):
         raise SystemExit(f"{len(f) - i} dispatches left unmatched")
     agg, by_shape = {}, {}
-    for (nf, vf), (nw, vw), (kind, alg, shape) in matched:
+    for (nf, vf), (nw, vw), (kind, alg, shape, tag) in matched:
         assert nf == nw and (("wgrad" in nf) == (kind == "wgrad")), (nf, nw, kind)
-        name = nf.replace("void ", "").split("(")[0]
-        for a in (agg.setdefault(name, [0.0, 0.0, 0.0, 0]), by_shape.setdefault((shape, kind), [0.0, 0.0, 0.0, 0])):
+        name = nf.replace("void ", "").split("(")[0] + tag
+        for a in (agg.setdefault(name, [0.0, 0.0, 0.0, 0]), by_shape.setdefault((shape, kind + tag), [0.0, 0.0, 0.0, 0])):
             a[0] += vf
             a[1] += vw
             a[2] += alg
@@ -203,7 +212,7 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
         out.append(f"traffic_bytes_per_launch {name} = {(vf + vw) / c:.0f}")
     out += ["", "Per shape (E, N, K) and direction, whole-tile kernel: fetch + write MB per launch / algorithmic MB"]
     for (shape, kind), (vf, vw, alg, c) in sorted(by_shape.items()):
-        out.append(f"  {shape[0]} {shape[1]:5d} {shape[2]:5d} {kind:5s} {vf / c / 1e6:8.1f} + {vw / c / 1e6:6.1f}"
+        out.append(f"  {shape[0]} {shape[1]:5d} {shape[2]:5d} {kind:17s} {vf / c / 1e6:8.1f} + {vw / c / 1e6:6.1f}"
                    f" / {alg / c / 1e6:6.1f} = {(vf + vw) / alg:5.2f}")
     return "\n".join(out)
 
@@ -292,9 +301,11 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
     for text in open(bench_json):
         if text.startswith("{"):
             line = json.loads(text)
-    bench_calls = {}
+    bench_calls, native_calls = {}, {}
     if line and line.get("roofline"):
         bench_calls = {canon(k): v["launches"] for k, v in line["roofline"]["by_kernel"].items()}
+    if line and line.get("roofline_native"):
+        native_calls = {canon(k): v["launches"] for k, v in line["roofline_native"]["by_kernel"].items()}
     if trace_csv:
         out += ["", "Per call, from the kernel trace: the span of each call's GEMM dispatches (whole-tile kernel "
                     "and any split / quarter-tile / reduce launches), by the call's whole-tile kernel; the sweep's "
@@ -307,17 +318,24 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
             nb = bench_calls.get(canon(name))
             if nb and len(cold) >= nb:
                 text += f";  the sweep's first {nb}: avg {sum(cold[:nb]) / nb / 1e3:9.2f} us"
+                nn = native_calls.get(canon(name))
+                if nn and len(cold) >= nb + nn:
+                    text += f";  the native sweep's {nn} after them: avg {sum(cold[nb:nb + nn]) / nn / 1e3:9.2f} us"
             out.append(text)
     if line and line.get("roofline"):
-        rf = line["roofline"]
         out += ["", "Same run, bench.py's own figures (HIP events on the launch stream, timed reps only):"]
-        for name, v in sorted(rf["by_kernel"].items()):
-            out.append(f"  {name:58s} avg {v['avg_launch_us']:9.2f} us over {v['launches']:5d} launches, "
-                       f"{v['tflops']:7.1f} TFLOP/s")
-        out.append(f"  dominant kernel {rf['kernel']}: achieved {rf['achieved']} TFLOP/s = {rf['frac']} of "
-                   f"{rf['peak']} (dense MXFP8), {rf['avg_launch_us']} us per call ({rf.get('scope', '')})")
+        for key, tag in (("roofline", ""), ("roofline_native", NATIVE_TAG)):
+            rf = line.get(key)
+            if not rf:
+                continue
+            for name, v in sorted(rf["by_kernel"].items()):
+                out.append(f"  {name + tag:70s} avg {v['avg_launch_us']:9.2f} us over {v['launches']:5d} launches, "
+                           f"{v['tflops']:7.1f} TFLOP/s")
+            out.append(f"  dominant kernel {rf['kernel']}{tag}: achieved {rf['achieved']} TFLOP/s = {rf['frac']} of "
+                       f"{rf['peak']} (dense MXFP8), {rf['avg_launch_us']} us per call ({rf.get('scope', '')})")
         out.append(f"  headline: fwd geomean {line['fwd_geomean_tflops']}  dgrad {line['dgrad_geomean_tflops']}  "
-                   f"wgrad {line['wgrad_geomean_tflops']} TFLOP/s")
+                   f"wgrad {line['wgrad_geomean_tflops']} TFLOP/s; kernel-only {line.get('kernel_only_geomean_tflops')}"
+                   f"; native layout {line.get('native_geomean_tflops')}")
     return "\n".join(out)
 
 
@@ -358,6 +376,80 @@ def cpu_baseline(budget_s: float):
             "sample": f"oracle fwd (dequantize e4m3+e8m0 -> fp32 matmul -> bf16), E=1, M={rows}, "
                       f"N=K=2048, {reps} reps in {t_total:.1f}s, numpy/BLAS threads={threads}, "
                       f"cpu={platform.processor() or platform.machine()}"}
+
+
+NATIVE_TAG = " [row pairs]"
+
+
+def kernel_geomeans(rows, suffix):
+    """{fwd, dgrad, wgrad}: geomean TFLOP/s over the rows of the per-call
+    times stored under ``<direction><suffix>`` (None when a row lacks one)."""
+    return {d: (round(geomean([r["M"] * 2.0 * r["N"] * r["K"] / (r[d + suffix] * 1e-6) / 1e12 for r in rows]), 1)
+                if rows and all(d + suffix in r for r in rows) else None)
+            for d in ("fwd", "dgrad", "wgrad")}
+
+
+def make_roofline(stats, tag, scope):
+    """Roofline of the dominant device kernel of `stats` (largest summed
+    time over the timed reps): algorithmic FLOPs 2*M*N*K per call / the mean
+    time of the call's GEMM launches (HIP events on the launch stream; the
+    split / quarter-tile tails included).  tag: suffix of the kernel's entry
+    in the committed HBM-traffic summary."""
+    if not stats:
+        return None
+    kname, k = max(stats.items(), key=lambda kv: kv[1]["ms"])
+    achieved = k["flops"] / (k["ms"] * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MXFP8_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4),
+            "traffic": read_traffic(kname + tag), "kernel": kname, "scope": scope,
+            "avg_launch_us": round(k["ms"] / k["launches"] * 1e3, 2),
+            "flops_per_launch": round(k["flops"] / k["launches"]),
+            "launches": k["launches"],
+            "by_kernel": {n: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 2),
+                              "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
+                              "launches": v["launches"]} for n, v in stats.items()}}
+
+
+def native_sweep(dev, args, flush, shapes, offs_by_shape, rows, account):
+    """The sweep's calls on the native operand layout: step-major scales and
+    row-pair data from the quantizers (``data_layout="pairs"``), GEMM launches
+    only between the events.  Stores ``<direction>_native_us`` in the sweep's
+    rows and accounts each call to `account`."""
+    import torch
+    from kernels import to_mx, to_mx_dim0, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
+    from kernels.forward import _pick_config
+    lay = {"scale_layout": "steps", "data_layout": "pairs"}
+    by_shape = {(r["E"], r["N"], r["K"]): r for r in rows}
+    for (E, N, K) in shapes:
+        M = M_TOKENS
+        offs = offs_by_shape[(E, N, K)]
+        flops = 2.0 * M * N * K
+        row = by_shape[(E, N, K)]
+
+        def timed(key, fn, kernel):
+            med, mean = time_call(fn, args.steps, args.warmup, flush)
+            row[key] = med * 1e3
+            account(kernel, mean, flops)
+
+        if args.only in ("all", "fwd"):
+            ta, pa = to_mx(torch.randn((M, K), device=dev).to(torch.bfloat16), **lay)
+            tw, pw = to_mx((torch.randn((E, N, K), device=dev) * 0.02).to(torch.bfloat16), **lay)
+            timed("fwd_native_us", lambda: triton_mxfp8_grouped_mm(pa, pw, ta, tw, offs),
+                  fwd_kernel_name(_pick_config(E, M, N, K)))
+            del ta, pa, tw, pw
+        if args.only in ("all", "dgrad"):
+            tg, pg = to_mx(torch.randn((M, N), device=dev).to(torch.bfloat16), **lay)
+            tt, pt = to_mx((torch.randn((E, K, N), device=dev) * 0.02).to(torch.bfloat16), **lay)
+            timed("dgrad_native_us", lambda: triton_mxfp8_grouped_mm(pg, pt, tg, tt, offs),
+                  fwd_kernel_name(_pick_config(E, M, K, N)))
+            del tg, pg, tt, pt
+        if args.only in ("all", "wgrad"):
+            tg, pg = to_mx_dim0(torch.randn((M, N), device=dev).to(torch.bfloat16), **lay)
+            ti, pi = to_mx_dim0(torch.randn((M, K), device=dev).to(torch.bfloat16), **lay)
+            timed("wgrad_native_us", lambda: triton_mxfp8_wgrad(pg, tg, pi, ti, offs), WGRAD_KERNEL)
+            del tg, pg, ti, pi
+        torch.cuda.empty_cache()
+        log(json.dumps({"E": E, "N": N, "K": K, **{k: round(v, 1) for k, v in row.items() if k.endswith("_native_us")}}))
 
 
 def extra_measurements(dev, args, flush):
@@ -425,7 +517,8 @@ def ep_shard_measurement(dev, args, flush):
     8 GPUs leaves one expert and about M/8 = 2080 tokens per GPU, so each
     (N, K) of the sweep becomes an E=1, M=2080 problem (a few hundred tiles,
     where the last round's handling decides the time).  Forward and wgrad,
-    drop-in calls, geomean TFLOP/s over the 9 (N, K)."""
+    drop-in calls, geomean TFLOP/s over the 9 (N, K); beside them the same
+    calls on the native layout (step-major scales, row-pair data)."""
     import torch
     from kernels import to_mx, to_mx_dim0, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
     M = M_TOKENS // 8
@@ -440,17 +533,28 @@ def ep_shard_measurement(dev, args, flush):
         sw, qw = to_mx(w)
         sg, qg = to_mx_dim0(go)
         si, qi = to_mx_dim0(a)
+        lay = {"scale_layout": "steps", "data_layout": "pairs"}
+        ta, pa = to_mx(a, **lay)
+        tw, pw = to_mx(w, **lay)
+        tg, pg = to_mx_dim0(go, **lay)
+        ti, pi = to_mx_dim0(a, **lay)
         flops = 2.0 * M * n * k
         fmed, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs), args.steps, args.warmup, flush)
         wmed, _ = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs), args.steps, args.warmup, flush)
-        rows.append({"N": n, "K": k, "fwd_us": round(fmed * 1e3, 1), "fwd_tflops": round(flops / (fmed * 1e-3) / 1e12, 1),
-                     "wgrad_us": round(wmed * 1e3, 1), "wgrad_tflops": round(flops / (wmed * 1e-3) / 1e12, 1)})
-        del a, w, go, sa, qa, sw, qw, sg, qg, si, qi
+        fnat, _ = time_call(lambda: triton_mxfp8_grouped_mm(pa, pw, ta, tw, offs), args.steps, args.warmup, flush)
+        wnat, _ = time_call(lambda: triton_mxfp8_wgrad(pg, tg, pi, ti, offs), args.steps, args.warmup, flush)
+        tf = lambda ms: round(flops / (ms * 1e-3) / 1e12, 1)
+        rows.append({"N": n, "K": k, "fwd_us": round(fmed * 1e3, 1), "fwd_tflops": tf(fmed),
+                     "wgrad_us": round(wmed * 1e3, 1), "wgrad_tflops": tf(wmed),
+                     "fwd_native_tflops": tf(fnat), "wgrad_native_tflops": tf(wnat)})
+        del a, w, go, sa, qa, sw, qw, sg, qg, si, qi, ta, pa, tw, pw, tg, pg, ti, pi
     torch.cuda.empty_cache()
     return {"workload": "E=1, M=2080 (16640 tokens / 8 GPUs), N, K in (2048, 5120, 8192): one GPU's expert-parallel "
                         "share of the sweep's E=8 shapes, drop-in calls",
             "fwd_geomean_tflops": round(geomean([r["fwd_tflops"] for r in rows]), 1),
             "wgrad_geomean_tflops": round(geomean([r["wgrad_tflops"] for r in rows]), 1),
+            "native_fwd_geomean_tflops": round(geomean([r["fwd_native_tflops"] for r in rows]), 1),
+            "native_wgrad_geomean_tflops": round(geomean([r["wgrad_native_tflops"] for r in rows]), 1),
             "rows": rows}
 
 
@@ -459,11 +563,12 @@ def moe_layer_measurement(dev, args, flush):
     forward and backward of MXFP8GroupedLinear(E=8, 5120 -> 8192) on 16640
     tokens (offsets random.seed(5)), i.e. to_mx_both of x, w and grad_out, the
     forward GEMM, dgrad and wgrad; 6*M*N*K FLOPs per step.  Beside it, the
-    three GEMMs alone on the same step-major operands, so the rest of the step
-    (quantization, allocation, autograd) is step - GEMMs."""
+    three GEMMs alone on operands in the layer's layouts (step-major scales,
+    row-pair data), so the rest of the step (quantization, allocation,
+    autograd) is step - GEMMs."""
     import torch
     from kernels import to_mx_both, triton_mxfp8_grouped_mm, triton_mxfp8_wgrad
-    from kernels.moe import MXFP8GroupedLinear
+    from kernels.moe import _LAYOUTS, MXFP8GroupedLinear
     from utils import generate_jagged_offs
     M, E, K, N = M_TOKENS, 8, 5120, 8192
     random.seed(5)
@@ -487,9 +592,9 @@ def moe_layer_measurement(dev, args, flush):
     x.grad = None
     layer.weight.grad = None
     with torch.no_grad():
-        (sx, qx), (sxt, qxt) = to_mx_both(x.detach(), scale_layout="steps")
-        (sw, qw), (swt, qwt) = to_mx_both(layer.weight.detach(), scale_layout="steps")
-        (sg, qg), (sgt, qgt) = to_mx_both(g, scale_layout="steps")
+        (sx, qx), (sxt, qxt) = to_mx_both(x.detach(), **_LAYOUTS)
+        (sw, qw), (swt, qwt) = to_mx_both(layer.weight.detach(), **_LAYOUTS)
+        (sg, qg), (sgt, qgt) = to_mx_both(g, **_LAYOUTS)
     gemm = {
         "fwd": time_call(lambda: triton_mxfp8_grouped_mm(qx, qw, sx, sw, offs), args.steps, args.warmup, flush)[0],
         "dgrad": time_call(lambda: triton_mxfp8_grouped_mm(qg, qwt, sg, swt, offs), args.steps, args.warmup,
@@ -518,6 +623,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-bf16", action="store_true",
                     help="skip the bf16 torch._grouped_mm arm of the forward (reference bench.py:159-161)")
+    ap.add_argument("--no-native", action="store_true",
+                    help="skip the second sweep on row-pair data (the native layout)")
+    ap.add_argument("--native-only", action="store_true",
+                    help="run only the sweep on row-pair data (for counter passes of that layout)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the BASELINE config 5 (e4m3 x e2m1) and quantizer measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -568,8 +677,8 @@ def main():
     # per device kernel: summed event time (ms), FLOPs and launches of the timed reps
     kstats = {}
 
-    def account(kernel, mean_ms, flops):
-        k = kstats.setdefault(kernel, {"ms": 0.0, "flops": 0.0, "launches": 0})
+    def account(kernel, mean_ms, flops, stats=kstats):
+        k = stats.setdefault(kernel, {"ms": 0.0, "flops": 0.0, "launches": 0})
         k["ms"] += mean_ms * args.steps
         k["flops"] += flops * args.steps
         k["launches"] += args.steps
@@ -587,6 +696,9 @@ def main():
         offs = offs_by_shape[(E, N, K)]
         flops = 2.0 * M * N * K
         row = {"E": E, "M": M, "N": N, "K": K}
+        if args.native_only:
+            rows.append(row)
+            continue
         if args.only in ("all", "fwd"):
             a = torch.randn((M, K), device=dev).to(torch.bfloat16)
             w = (torch.randn((E, N, K), device=dev) * 0.02).to(torch.bfloat16)
@@ -649,6 +761,12 @@ def main():
         rows.append(row)
         log(json.dumps({k: (round(v, 1) if isinstance(v, float) else v) for k, v in row.items()}))
 
+    # the sweep again on row-pair data (after the whole row-major sweep, so
+    # that a kernel trace lists the row-major kernel-only calls first)
+    nstats = {}
+    if not args.no_native or args.native_only:
+        native_sweep(dev, args, flush, shapes, offs_by_shape, rows,
+                     lambda kernel, mean_ms, flops: account(kernel, mean_ms, flops, nstats))
     extra = None if args.no_extra else extra_measurements(dev, args, flush)
 
     def gm(key):
@@ -668,24 +786,15 @@ def main():
     # reps): algorithmic FLOPs 2*M*N*K per call / the mean time of the call's
     # GEMM launches on step-major scales (HIP events on the launch stream; no
     # re-layout launch between them, the split / quarter-tile tails included)
-    roofline = None
-    if kstats:
-        kname, k = max(kstats.items(), key=lambda kv: kv[1]["ms"])
-        achieved = k["flops"] / (k["ms"] * 1e-3) / 1e12
-        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MXFP8_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4),
-                    "traffic": read_traffic(kname), "kernel": kname,
-                    "scope": "GEMM launches of one call on step-major scales: the whole-tile kernel, plus the "
-                             "piece / quarter-tile / reduce launches of a split last round",
-                    "avg_launch_us": round(k["ms"] / k["launches"] * 1e3, 2),
-                    "flops_per_launch": round(k["flops"] / k["launches"]),
-                    "launches": k["launches"],
-                    "by_kernel": {n: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 2),
-                                      "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
-                                      "launches": v["launches"]} for n, v in kstats.items()}}
+    roofline = make_roofline(kstats, "", "GEMM launches of one call on step-major scales and row-major data: "
+                                         "the whole-tile kernel, plus the piece / quarter-tile / reduce launches "
+                                         "of a split last round")
+    roofline_native = make_roofline(nstats, NATIVE_TAG, "the same launches on row-pair data (native layout)")
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
     value = fwd_gm if fwd_gm is not None else (dgrad_gm or wgrad_gm)
+    if value is None:            # --native-only: nothing row-major was timed
+        value = next((v for v in kernel_geomeans(rows, "_native_us").values() if v), 0.0)
     line = {
         "metric": "geomean MXFP8 grouped-GEMM TFLOPs (% of MXFP8 peak), fwd/dgrad/wgrad, 1 GPU",
         "value": round(value, 1),
@@ -714,10 +823,11 @@ def main():
         "fwd_speedup_vs_bf16_geomean": round(speedup_gm, 3) if speedup_gm else None,
         "fwd_speedup_vs_readme_bf16": round(fwd_gm / REF_BF16_GEOMEAN_TFLOPS, 3) if fwd_gm else None,
         "ref_speedup_vs_bf16_geomean": REF_SPEEDUP_VS_BF16,
-        "kernel_only_geomean_tflops": {d: (round(geomean([r["M"] * 2.0 * r["N"] * r["K"] / (r[d + "_kernel_us"] * 1e-6)
-                                                          / 1e12 for r in rows]), 1)
-                                           if rows and all(d + "_kernel_us" in r for r in rows) else None)
-                                       for d in ("fwd", "dgrad", "wgrad")},
+        "kernel_only_geomean_tflops": kernel_geomeans(rows, "_kernel_us"),
+        "native_geomean_tflops": kernel_geomeans(rows, "_native_us"),
+        "native_layout": "kernel-only time on the layout the kernels read fastest: step-major scales and row-pair "
+                         "e4m3 data (rows 2i, 2i+1 interleaved in 64-byte pieces), both written by the quantizers "
+                         "outside the timed region; same bits as the row-major calls",
         "cfg5_mxfp4": extra["cfg5"] if extra else None,
         "quantizer": extra["quant"] if extra else None,
         "moe_layer": extra["moe_layer"] if extra else None,
@@ -725,6 +835,7 @@ def main():
         "fwd_geomean_by_E": per_e,
         "baseline_note": "vs_baseline = fwd geomean / 1498.8 TFLOP/s (reference README table, MI355X)",
         "roofline": roofline,
+        "roofline_native": roofline_native,
         "cpu_baseline": cpu,
         "wall_s": round(time.time() - t_start, 1),
     }
