@@ -411,13 +411,16 @@ __device__ __forceinline__ void finish_scales(uint32_t (&xs)[C::FM], uint32_t (&
   for (int j = 0; j < C::FN; ++j) ws[j] = out ? 127u : (ws[j] >> sh);
 }
 
-template <class C, int B, int E>
+// MFMAs B .. E-1 of a stage (fragment t: row block t / FN, column block
+// t % FN).  FIRST: the reduction's first stage, which starts each accumulator
+// from zero (the MFMA's C operand) instead of reading it.
+template <class C, int B, int E, bool FIRST = false>
 __device__ __forceinline__ void mfma_range(const Frags<C>& F, const uint32_t (&xs)[C::FM],
                                            const uint32_t (&ws)[C::FN], v16f (&acc)[C::FM][C::FN]) {
 #pragma unroll
   for (int t = B; t < E; ++t) {
     const int i = t / C::FN, j = t % C::FN;
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.a[j], F.b[i], acc[i][j], C::WFMT,
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.a[j], F.b[i], FIRST ? (v16f){} : acc[i][j], C::WFMT,
                                                                  MXGG_FMT_E4M3, 0, (int)ws[j], 0, (int)xs[i]);
   }
 }
@@ -463,7 +466,8 @@ __device__ __forceinline__ void interleave_step() {
 // (Fn, xn, wn), start the copies of stage s0 + r + NS and, when stage
 // s0 + r + 1 opens a scale group, the scales of the group after it.
 // (s0 is the ring's first stage, even, in slot 0; t0 = s0 / 2 its step.)
-template <class C>
+// FIRST: stage s0, whose MFMAs start the accumulators from zero.
+template <class C, bool FIRST = false>
 __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, const Operand& W,
                                            __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P, int s0, int r,
                                            int lo, int hi, Frags<C>& Fc, uint32_t (&xc)[C::FM],
@@ -476,7 +480,7 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   uint8_t* cur = smem + (r % C::NS) * C::STAGE;
   const uint8_t* nxt = smem + (rn % C::NS) * C::STAGE;
   const uint8_t* snx = smem + C::SOFF + ((rn / SPG) & 1) * C::SSLOT;
-  mfma_range<C, 0, NE>(Fc, xc, wc, acc);
+  mfma_range<C, 0, NE, FIRST>(Fc, xc, wc, acc);
   MXGG_SCHED_FENCE();
   MXGG_WAIT_VM((C::NS - 2) * C::LPS);       // this wave's copies of stage r+1 have landed
   MXGG_BARRIER();                           // ... every wave's; and stage r's slot is free
@@ -493,7 +497,7 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   const bool opens = rn % SPG == 0 && tg * STEP < hi;
   issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, ssr, P, tg, opens);
   issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
-  mfma_range<C, NE, NMMA>(Fc, xc, wc, acc);
+  mfma_range<C, NE, NMMA, FIRST>(Fc, xc, wc, acc);
   interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, C::LPS>();
   MXGG_SCHED_FENCE();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -503,16 +507,29 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   MXGG_SCHED_FENCE();
 }
 
+template <class C>
+__device__ __forceinline__ void zero_acc(v16f (&acc)[C::FM][C::FN]) {
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
+}
+
 // Reduction over the 64-element stages [s0, s1) restricted to the element
-// range [lo, hi) (chunks and scale blocks outside it are zero / neutral).
+// range [lo, hi) (chunks and scale blocks outside it are zero / neutral),
+// into acc.  ZSTART: the first stage's MFMAs start from zero, so acc needs no
+// clearing (256 accumulator writes per lane, which the compiler otherwise puts
+// between the tile set-up and the first copies, twice over when an empty range
+// has a path of its own); else the caller zeroes acc.  An empty range runs one
+// stage wholly outside [lo, hi).
 // The ring starts at the even stage s0 & ~1 so that scale groups cover whole
 // steps; an odd stage count runs one stage past s1.  Those extra stages are
 // wholly outside [lo, hi): zero data, neutral scales, exactly zero added.
-template <class C>
+template <class C, bool ZSTART = true>
 __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, const Operand& W,
                                               const ScaleSrc& xss, const ScaleSrc& wss, int s0, int s1,
                                               int lo, int hi, v16f (&acc)[C::FM][C::FN]) {
-  if (s0 >= s1) return;
+  if (s0 >= s1) s1 = s0 + 1;
   s0 &= ~1;
   Plan<C> P;
   make_plan<C>(P, X, W, xss, wss);
@@ -532,8 +549,14 @@ __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, c
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   finish_scales<C>(xa, wa, s0, lo, hi);
   const int n = s1 - s0;
+  int r0 = 0;
+  if constexpr (ZSTART) {
+    ring_stage<C, true>(smem, X, W, ssr, P, s0, 0, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+    ring_stage<C>(smem, X, W, ssr, P, s0, 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    r0 = 2;
+  }
 #pragma nounroll
-  for (int r = 0; r < n; r += 2) {
+  for (int r = r0; r < n; r += 2) {
     ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
     ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
   }
@@ -1009,12 +1032,7 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
   const ScaleSrc xs{make_rsrc(p.as, p.as_bytes), (uint32_t)p.M, (uint32_t)row0};
   const ScaleSrc ws{make_rsrc(p.bs + (int64_t)tl.expert * p.bs_expert, p.bs_expert), (uint32_t)p.N, (uint32_t)n0};
 
-  v16f acc[C::FM][C::FN];
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
-
+  v16f acc[C::FM][C::FN];   // set by ring_mainloop
   const int K = (int)p.K;
   if constexpr (PIECES) {
     int a, b;
@@ -1024,7 +1042,14 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
     ring_mainloop<C>(smem, X, W, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
     store_partial<C>(acc, p.part + (int64_t)slot * (C::BM * C::BN));
   } else {
-    ring_mainloop<C>(smem, X, W, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
+    // the f32 epilogue's register allocation spills when the first stage is
+    // peeled: it keeps the accumulators zeroed up front
+    if constexpr (EPI == kEpiF32) {
+      zero_acc<C>(acc);
+      ring_mainloop<C, false>(smem, X, W, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
+    } else {
+      ring_mainloop<C>(smem, X, W, xs, ws, 0, (K + BKS - 1) / BKS, 0, K, acc);
+    }
     if constexpr (EPI == kEpiBf16) {
       store_tile_lds<C, true>(acc, smem, p.out + (row0 * p.ldo + n0) * 2, p.ldo, rows, cols);
     } else if constexpr (EPI == kEpiF16) {
@@ -1435,12 +1460,10 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   const ScaleSrc ws{make_rsrc(p.is, p.is_bytes), (uint32_t)p.K, (uint32_t)k0};
 
   v16f acc[C::FM][C::FN];
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
-
-  if (hi > lo) ring_mainloop<C>(smem, X, W, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
+  if (hi > lo)
+    ring_mainloop<C>(smem, X, W, xs, ws, lo / BKS, (hi + BKS - 1) / BKS, lo, hi, acc);
+  else
+    zero_acc<C>(acc);
   // group bounds that are not multiples of 16 (any offsets are accepted, as
   // in the reference): the straddling chunks' in-group tokens
   if ((lo | hi) & 15) edge_chunks<C>(X, W, xs, ws, lo, hi, acc);
