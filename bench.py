@@ -454,8 +454,9 @@ def native_sweep(dev, args, flush, shapes, offs_by_shape, rows, account):
 
 def extra_measurements(dev, args, flush):
     """BASELINE config 5 (MXFP8 x MXFP4 forward, E=8, M=16640, N=8192,
-    K=5120, offsets drawn with random.seed(4)) as a drop-in call and as
-    kernel-only time, and the quantizer's bandwidth on the sweep's largest
+    K=5120, offsets drawn with random.seed(4)) as a drop-in call, as
+    kernel-only time and on the native layout (row pairs / row quads), and
+    the quantizer's bandwidth on the sweep's largest
     activation (16640 x 8192 bf16): to_mx (2 + 1 + 1/32 B per element),
     to_mx_dim0 (the same bytes, transposed output) and to_mx_both (both
     layouts from one read: 2 + 2 * (1 + 1/32) B per element)."""
@@ -471,19 +472,22 @@ def extra_measurements(dev, args, flush):
     fp4 = torch.float4_e2m1fn_x2
     sa, qa = to_mx(a)
     sw, qw = to_mx(w, elem_dtype=fp4)
-    ta, _ = to_mx(a, scale_layout="steps")
-    tw, _ = to_mx(w, elem_dtype=fp4, scale_layout="steps")
+    ta, pa = to_mx(a, scale_layout="steps", data_layout="pairs")
+    tw, pw = to_mx(w, elem_dtype=fp4, scale_layout="steps", data_layout="quads")
     del a, w
     flops = 2.0 * M * N * K
     med, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs), args.steps, args.warmup, flush)
     kmed, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs), args.steps, args.warmup, flush)
+    nmed, _ = time_call(lambda: triton_mxfp8_grouped_mm(pa, pw, ta, tw, offs), args.steps, args.warmup, flush)
     tf = flops / (med * 1e-3) / 1e12
     cfg5 = {"workload": "BASELINE config 5: e4m3 activations x e2m1 weights, E=8, M=16640, N=8192, K=5120, "
                         "offs random.seed(4)",
             "us": round(med * 1e3, 1), "tflops": round(tf, 1),
             "frac_of_mxfp4_peak": round(tf / PEAK_MXFP4_TFLOPS, 4), "frac_of_mxfp8_peak": round(tf / PEAK_MXFP8_TFLOPS, 4),
-            "kernel_only_us": round(kmed * 1e3, 1), "kernel_only_tflops": round(flops / (kmed * 1e-3) / 1e12, 1)}
-    del qa, qw, sa, sw, ta, tw
+            "kernel_only_us": round(kmed * 1e3, 1), "kernel_only_tflops": round(flops / (kmed * 1e-3) / 1e12, 1),
+            "native_us": round(nmed * 1e3, 1), "native_tflops": round(flops / (nmed * 1e-3) / 1e12, 1),
+            "native_layout": "activations in row pairs, e2m1 weights in row quads, step-major scales"}
+    del qa, qw, sa, sw, ta, tw, pa, pw
     torch.cuda.empty_cache()
     x = torch.randn((M, 8192), device=dev).to(torch.bfloat16)
     n = x.numel()

@@ -181,21 +181,24 @@ __device__ __forceinline__ int swz4(int r) {
 }
 __device__ __forceinline__ int swz2(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
-// A tile's rows of one operand in global memory, in one of two layouts:
+// A tile's rows of one operand in global memory, in one of three layouts,
+// G = 2**pl rows per group:
 //   rows  (pl = 0): byte k of row r at r * ld + k;
-//   pairs (pl = 1): rows 2i and 2i+1 interleave in 64-byte pieces, byte k of
-//         row r at (r / 2) * 2 ld + (k / 64) * 128 + (r % 2) * 64 + k % 64,
-//         so the 64-byte stage pieces of two adjacent rows fill one 128-byte
-//         line and a 16-row copy touches 8 whole lines instead of 16 halves.
+//   pairs (pl = 1, e4m3) and quads (pl = 2, packed e2m1): the G rows of a
+//         group interleave in P = 128 / G byte pieces -- one 64-element
+//         stage of a row -- byte k of row r at (r / G) * G ld +
+//         (k / P) * 128 + (r % G) * P + k % P, so the stage pieces of a group
+//         fill one 128-byte line and a copy touches whole lines instead of
+//         halves (pairs) or quarters (quads).
 // Local row r of the tile is row e = r + shift of the buffer `data`, which
-// starts at the tile's first row (rows) or first pair (pairs: shift = row0 %
-// 2); the range ends after the pair of the tile's last row, so reads past the
-// tile's rows return 0 except the partner row of a last, odd row.
+// starts at the group of the tile's first row (shift = row0 % G); the range
+// ends after the group of the tile's last row, so reads past the tile's rows
+// return 0 except the other rows of that last group.
 struct Operand {
   __amdgpu_buffer_rsrc_t data;
-  uint32_t ld;                   // rows: bytes between rows; pairs: half the bytes between pairs
-  uint32_t pl;                   // layout: 0 rows, 1 pairs
-  uint32_t shift;                // pairs: row0 % 2 of the tile; rows: 0
+  uint32_t ld;                   // bytes between rows (groups: between groups / G)
+  uint32_t pl;                   // log2 G: 0 rows, 1 pairs, 2 quads
+  uint32_t shift;                // row0 % G of the tile
 };
 
 // Operand of rows row0 .. row0 + rows - 1 of the matrix at `base`.
@@ -203,17 +206,21 @@ __device__ __forceinline__ Operand make_operand(const uint8_t* base, int64_t ld,
   Operand o;
   o.ld = (uint32_t)ld;
   o.pl = (uint32_t)pl;
-  o.shift = (uint32_t)(row0 & pl);
-  const int64_t unit = ld << pl;                                  // bytes per row (pair)
-  const uint32_t units = (uint32_t)(((int64_t)o.shift + rows + pl) >> pl);
+  const int64_t mask = ((int64_t)1 << pl) - 1;
+  o.shift = (uint32_t)(row0 & mask);
+  const int64_t unit = ld << pl;                                  // bytes per group
+  const uint32_t units = (uint32_t)(((int64_t)o.shift + rows + mask) >> pl);
   o.data = make_rsrc(base + (row0 >> pl) * unit, units * (uint32_t)unit);
   return o;
 }
 
-// Byte offset in O.data of byte `col` of local row `row`.
+// Byte offset in O.data of byte `col` of local row `row` (pieces of
+// 2**pb = 128 / G bytes; for rows, pb = 7 leaves col unchanged).
 __device__ __forceinline__ uint32_t operand_off(const Operand& O, uint32_t row, uint32_t col) {
   const uint32_t e = row + O.shift;
-  return (e >> O.pl) * (O.ld << O.pl) + ((col >> 6) << (6 + O.pl)) + ((e & O.pl) << 6) + (col & 63u);
+  const uint32_t pb = 7u - O.pl;
+  return (e >> O.pl) * (O.ld << O.pl) + ((col >> pb) << 7) + ((e & ((1u << O.pl) - 1u)) << pb) +
+         (col & ((1u << pb) - 1u));
 }
 
 // Where a tile's step-major scales live: dword (t, r) of an operand with R
@@ -949,7 +956,7 @@ struct FwdParams {
   int grid_n; int group_m; int xcd;
   float* part; int par; int slots;          // split: partial slots, resident workgroups, slot count
   int quads;                                // last round as 128 x 128 quarter tiles (quad_dp)
-  int a_pl; int b_pl;                       // operand layouts: 0 rows, 1 row pairs (Operand)
+  int a_pl; int b_pl;                       // operand layouts: 0 rows, 1 row pairs, 2 row quads (Operand)
 };
 
 // Epilogue of the whole-tile kernels, fixed at compile time so that the
@@ -1856,9 +1863,9 @@ extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, in
   return part ? align256(sc) + part : sc;
 }
 
-// Bytes a row of `len` bytes takes in an operand of layout flag `pairs`: the
-// row-pair layout stores whole 64-byte pieces.
-static int64_t operand_row_bytes(int64_t len, bool pairs) { return pairs ? (len + 63) / 64 * 64 : len; }
+// Bytes a row of `len` bytes takes in an operand stored in pieces of `piece`
+// bytes (64 for row pairs, 32 for row quads, 1 for rows).
+static int64_t operand_row_bytes(int64_t len, int64_t piece) { return (len + piece - 1) / piece * piece; }
 
 // Argument checks of a forward call shared by the entry points; MXGG_OK
 // when the call may go ahead (check *empty: nothing to compute).
@@ -1871,13 +1878,16 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
   *empty = false;
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: weight format %d not E4M3/E2M1", b_fmt);
-  if (layout & ~(MXGG_A_PAIRS | MXGG_B_PAIRS))
+  if (layout & ~(MXGG_A_PAIRS | MXGG_B_PAIRS | MXGG_B_QUADS) || (layout & MXGG_B_PAIRS && layout & MXGG_B_QUADS))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: unknown operand layout flags %d", layout);
-  const bool ap = layout & MXGG_A_PAIRS, bp = layout & MXGG_B_PAIRS;
+  const bool ap = layout & MXGG_A_PAIRS, bp = layout & MXGG_B_PAIRS, bq = layout & MXGG_B_QUADS;
   if (bp && b_fmt != MXGG_FMT_E4M3)
-    return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: row pairs are built for e4m3 weights only");
-  if ((ap && M % 2) || (bp && N % 2))
-    return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: an operand in row pairs needs an even row count (M=%lld, N=%lld)",
+    return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: row pairs are built for e4m3 weights only (e2m1: row quads)");
+  if (bq && b_fmt != MXGG_FMT_E2M1)
+    return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: row quads are built for packed e2m1 weights only (e4m3: row pairs)");
+  if ((ap && M % 2) || (bp && N % 2) || (bq && N % 4))
+    return fail(MXGG_ERR_INVALID_ARG,
+                "grouped_mm: an operand in row pairs / quads needs a row count divisible by 2 / 4 (M=%lld, N=%lld)",
                 (long long)M, (long long)N);
   if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F16 && out_dtype != MXGG_DTYPE_F32)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: out_dtype %d not BF16/F16/F32", out_dtype);
@@ -1885,7 +1895,7 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: negative shape");
   if (K % 32) return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: K=%lld must be a multiple of 32", (long long)K);
   const int64_t kb = b_fmt == MXGG_FMT_E2M1 ? K / 2 : K;
-  if (lda < operand_row_bytes(K, ap) || ldb_n < operand_row_bytes(kb, bp) || ldo < N ||
+  if (lda < operand_row_bytes(K, ap ? 64 : 1) || ldb_n < operand_row_bytes(kb, bp ? 64 : (bq ? 32 : 1)) || ldo < N ||
       (plain && (ldas < K / 32 || ldbs_n < K / 32)))
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm: a row stride is smaller than its row");
   if (E > 1 && (ldb_e < N * ldb_n || (plain && ldbs_e < N * ldbs_n)))
@@ -1922,7 +1932,7 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
   float* part = c.split && part_area && part_bytes ? (float*)part_area : nullptr;
   FwdParams p{A, lda, B, ldb_n, ldb_e, as, (uint32_t)(4 * T * M), bs, (uint32_t)(4 * T * N), offs, E, M, N, K,
               (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0, 0,
-              (layout & MXGG_A_PAIRS) ? 1 : 0, (layout & MXGG_B_PAIRS) ? 1 : 0};
+              (layout & MXGG_A_PAIRS) ? 1 : 0, (layout & MXGG_B_PAIRS) ? 1 : ((layout & MXGG_B_QUADS) ? 2 : 0)};
   const size_t pb = part ? part_bytes : 0;
   if (b_fmt == MXGG_FMT_E2M1)
     return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
@@ -2117,7 +2127,7 @@ static int check_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, 
   if ((gp && N % 2) || (ip && K % 2))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: an operand in row pairs needs an even row count (N=%lld, K=%lld)",
                 (long long)N, (long long)K);
-  if (ld_go < operand_row_bytes(M, gp) || ld_ia < operand_row_bytes(M, ip) ||
+  if (ld_go < operand_row_bytes(M, gp ? 64 : 1) || ld_ia < operand_row_bytes(M, ip ? 64 : 1) ||
       (plain && (ld_gos < M / 32 || ld_ias < M / 32)))
     return fail(MXGG_ERR_INVALID_ARG, "wgrad: a row stride is smaller than its row");
   if (ld_go % 16 || ld_ia % 16 || !aligned16(go_t) || !aligned16(ia_t))

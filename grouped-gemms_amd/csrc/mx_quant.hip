@@ -31,9 +31,11 @@
 // E4M3 data goes out row-major or, on request (MXGG_DATA_PAIRS), in row
 // pairs: byte k of row r at (r/2) 2 ld + (k/64) 128 + (r%2) 64 + k%64, the
 // layout in which the GEMM's 64-element stage of two adjacent rows is one
-// 128-byte line.  Every store of these kernels (8 or 32 bytes at a multiple
-// of its size) stays inside one 64-byte piece, so only the address changes;
-// the pad of a row whose length is an odd multiple of 32 is written zero.
+// 128-byte line; packed E2M1 data (32 bytes per stage of a row) likewise in
+// row quads (MXGG_DATA_QUADS): (r/4) 4 ld + (k/32) 128 + (r%4) 32 + k%32.
+// Every store of these kernels (4, 8 or 32 bytes at a multiple of its size)
+// stays inside one piece, so only the address changes; the pad of a row
+// whose last piece is half full is written zero.
 #include "mxgg_device.h"
 #include "mxgg_host.h"
 
@@ -89,10 +91,12 @@ __device__ __forceinline__ uint32_t gather4(uint32_t s, int j) {
   return v;
 }
 
-// Offset of byte k of row r of a quantizer output with row stride ld, row
-// pairs when pl = 1 (k % 64 + the store's size <= 64).
+// Offset of byte k of row r of a quantizer output with row stride ld, in
+// groups of 2**pl rows interleaved in 128 >> pl byte pieces (pl = 0: rows;
+// 1: pairs; 2: quads; the store stays inside one piece).
 __device__ __forceinline__ int64_t q_off(int64_t r, int64_t k, int64_t ld, int pl) {
-  return pl ? (r >> 1) * (ld << 1) + ((k >> 6) << 7) + ((r & 1) << 6) + (k & 63) : r * ld + k;
+  const int pb = 7 - pl;
+  return (r >> pl) * (ld << pl) + ((k >> pb) << 7) + ((r & ((1 << pl) - 1)) << pb) + (k & ((1 << pb) - 1));
 }
 
 __device__ __forceinline__ void zero32(uint8_t* dst) {
@@ -206,8 +210,8 @@ __device__ __forceinline__ uint32_t quant32(const float (&v)[32], uint8_t* dst) 
 // contiguous 4 KB of bf16), one grid-stride pass per 64 * gridDim.x blocks.
 // When rows hold a multiple of 4 blocks, four consecutive quads' scale bytes
 // (one step of a row) go out as one dword.  I: the block index type (32-bit
-// when the block count fits: one cheap division per block).  pl: e4m3 output
-// in row pairs.
+// when the block count fits: one cheap division per block).  pl: output in
+// row pairs (e4m3, pl = 1) or row quads (e2m1, pl = 2).
 template <int SRC, int FMT, class I>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restrict__ src,
                                                          int64_t rows, int64_t cols,
@@ -255,7 +259,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint8_t* __restri
         uint32_t w = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) w |= e2m1_code(v[i], mul) << (4 * i);
-        *reinterpret_cast<uint32_t*>(q + (int64_t)r * ld_q + col / 2) = w;
+        *reinterpret_cast<uint32_t*>(q + q_off(r, col / 2, ld_q, pl)) = w;
+        // row quads, odd block count: the last block's lanes zero the pad
+        if (pl && (bpr & 1) && cb == bpr - 1) *reinterpret_cast<uint32_t*>(q + q_off(r, col / 2 + 16, ld_q, pl)) = 0u;
       }
     }
     if (by4) {
@@ -380,8 +386,10 @@ namespace {
 // Scale destination for `out_rows` rows of `nblk` blocks; MXGG_OK or a
 // failure naming `what`.
 int scale_out(const char* what, uint8_t* p, int64_t ld_s, int layout, int64_t out_rows, int64_t nblk, ScaleOut* o) {
-  if (layout & ~(MXGG_SCALES_STEPS | MXGG_DATA_PAIRS))
-    return fail(MXGG_ERR_INVALID_ARG, "%s: layout %d not PLAIN/STEPS, optionally | DATA_PAIRS", what, layout);
+  if (layout & ~(MXGG_SCALES_STEPS | MXGG_DATA_PAIRS | MXGG_DATA_QUADS) ||
+      ((layout & MXGG_DATA_PAIRS) && (layout & MXGG_DATA_QUADS)))
+    return fail(MXGG_ERR_INVALID_ARG, "%s: layout %d not PLAIN/STEPS, optionally | DATA_PAIRS or DATA_QUADS", what,
+                layout);
   layout &= MXGG_SCALES_STEPS;
   o->p = p;
   o->ld = ld_s;
@@ -398,13 +406,17 @@ int scale_out(const char* what, uint8_t* p, int64_t ld_s, int layout, int64_t ou
   return MXGG_OK;
 }
 
-// A data output of `rows` rows of `len` bytes in row pairs: even rows, row
-// stride a multiple of 64 that holds the row rounded up to 64.
-int pairs_out(const char* what, int64_t rows, int64_t len, int64_t ld) {
-  if (rows % 2) return fail(MXGG_ERR_INVALID_ARG, "%s: row pairs need an even row count, got %lld", what, (long long)rows);
-  if (ld % 64 || ld < (len + 63) / 64 * 64)
-    return fail(MXGG_ERR_INVALID_ARG, "%s: row pairs need a row stride that is a multiple of 64 and holds %lld bytes",
-                what, (long long)((len + 63) / 64 * 64));
+// A data output of `rows` rows of `len` bytes in groups of g rows (2: pairs,
+// 4: quads) of 128 / g byte pieces: rows divisible by g, row stride a
+// multiple of the piece that holds the row rounded up to it.
+int pairs_out(const char* what, int64_t rows, int64_t len, int64_t ld, int g = 2) {
+  const int64_t piece = 128 / g;
+  if (rows % g)
+    return fail(MXGG_ERR_INVALID_ARG, "%s: row %s need a row count divisible by %d, got %lld", what,
+                g == 2 ? "pairs" : "quads", g, (long long)rows);
+  if (ld % piece || ld < (len + piece - 1) / piece * piece)
+    return fail(MXGG_ERR_INVALID_ARG, "%s: row %s need a row stride that is a multiple of %lld and holds %lld bytes",
+                what, g == 2 ? "pairs" : "quads", (long long)piece, (long long)((len + piece - 1) / piece * piece));
   return MXGG_OK;
 }
 
@@ -426,10 +438,11 @@ extern "C" int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, in
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: row stride smaller than the row");
   ScaleOut so;
   if (int rc = scale_out("quantize_mx", scales, ld_s, scale_layout, rows, cols / 32, &so)) return rc;
-  const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : 0;
-  if (pl && elem_fmt != MXGG_FMT_E4M3) return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx: row pairs are built for e4m3 only");
+  const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : ((scale_layout & MXGG_DATA_QUADS) ? 2 : 0);
+  if ((pl == 1 && elem_fmt != MXGG_FMT_E4M3) || (pl == 2 && elem_fmt != MXGG_FMT_E2M1))
+    return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx: row pairs hold e4m3 data and row quads packed e2m1");
   if (pl) {
-    if (int rc = pairs_out("quantize_mx", rows, cols, ld_q)) return rc;
+    if (int rc = pairs_out("quantize_mx", rows, qcols, ld_q, 1 << pl)) return rc;
   }
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!src || !q || !scales) return fail(MXGG_ERR_INVALID_ARG, "quantize_mx: null pointer");
@@ -485,6 +498,8 @@ extern "C" int mxgg_quantize_mx_dim0(const void* src, int src_dtype, int64_t row
     return fail(MXGG_ERR_INVALID_ARG, "quantize_mx_dim0: row stride smaller than the row");
   ScaleOut so;
   if (int rc = scale_out("quantize_mx_dim0", scales, ld_s, scale_layout, cols, rows / 32, &so)) return rc;
+  if (scale_layout & MXGG_DATA_QUADS)
+    return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx_dim0: row quads hold packed e2m1 data; this output is e4m3");
   const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : 0;
   if (pl) {
     if (int rc = pairs_out("quantize_mx_dim0", cols, rows, ld_q)) return rc;
@@ -528,6 +543,8 @@ extern "C" int mxgg_quantize_mx_both(const void* src, int src_dtype, int64_t bat
   ScaleOut sr, sc;
   if (int rc = scale_out("quantize_mx_both", s_rows, ld_sr, scale_layout, batch * rows, cols / 32, &sr)) return rc;
   if (int rc = scale_out("quantize_mx_both", s_cols, ld_sc, scale_layout, batch * cols, rows / 32, &sc)) return rc;
+  if (scale_layout & MXGG_DATA_QUADS)
+    return fail(MXGG_ERR_UNSUPPORTED, "quantize_mx_both: row quads hold packed e2m1 data; these outputs are e4m3");
   const int pl = (scale_layout & MXGG_DATA_PAIRS) ? 1 : 0;
   if (pl) {
     if (int rc = pairs_out("quantize_mx_both", rows, cols, ld_qr)) return rc;

@@ -12,7 +12,7 @@ reference quantizes with eager torch ops in utils.py:67-105), whose
 GEMMs copy in whole 128-byte lines.
 """
 
-from ._common import _rocm_mxfp8_available, to_row_pairs
+from ._common import _rocm_mxfp8_available, to_row_pairs, to_row_quads
 from .backward import triton_mxfp8_wgrad
 from .forward import triton_mxfp8_grouped_mm
 from .moe import MXFP8GroupedLinear, mxfp8_grouped_mm
@@ -26,6 +26,7 @@ __all__ = [
     "to_mx_dim0",
     "to_mx_both",
     "to_row_pairs",
+    "to_row_quads",
     "mxfp8_grouped_mm",
     "MXFP8GroupedLinear",
 ]

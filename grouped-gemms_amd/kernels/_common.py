@@ -52,37 +52,54 @@ def _out_code(dtype: torch.dtype, allowed=(torch.bfloat16, torch.float16, torch.
     return _OUT_CODES[dtype]
 
 
-def _pair_buffer(batch: tuple, rows: int, length: int, device) -> tuple:
-    """Fresh uint8 row-pair storage for ``(*batch, rows, length)`` data.
+def _pair_buffer(batch: tuple, rows: int, length: int, device, group: int = 2) -> tuple:
+    """Fresh uint8 row-group storage for ``(*batch, rows, length)`` data.
 
-    Row pairs (``MXGG_DATA_PAIRS``, no counterpart in the reference): with
-    ``ld = length`` rounded up to 64, byte k of row r sits at
-    ``(r // 2) * 2 * ld + (k // 64) * 128 + (r % 2) * 64 + k % 64``, so the
-    64-byte pieces of two adjacent rows that the GEMMs stage together form
+    Row pairs (``group`` 2, e4m3: ``MXGG_DATA_PAIRS``) and row quads (4,
+    packed e2m1: ``MXGG_DATA_QUADS``), a layout with no counterpart in the
+    reference: with pieces of ``P = 128 // group`` bytes (one 64-element
+    stage of a row) and ``ld = length`` rounded up to P, byte k of row r sits
+    at ``(r // group) * group * ld + (k // P) * 128 + (r % group) * P + k % P``,
+    so the pieces of the rows of a group that the GEMMs stage together form
     one 128-byte line.  Returned as the strided view
-    ``(*batch, rows // 2, 2, ld // 64, 64)`` -- element ``[.., p, h, s, b]`` is
-    byte ``64 s + b`` of row ``2 p + h`` -- so ``view.reshape(*batch, rows,
-    ld)`` gives the rows back (with the pad bytes past ``length``).  Returns
-    ``(view, ld)``."""
-    if rows % 2:
-        raise ValueError(f"row pairs need an even row count, got {rows}")
-    ld = (length + 63) // 64 * 64
-    buf = torch.empty(tuple(batch) + (rows // 2, ld // 64, 2, 64), dtype=torch.uint8, device=device)
+    ``(*batch, rows // group, group, ld // P, P)`` -- element ``[.., g, h, s, b]``
+    is byte ``P s + b`` of row ``group g + h`` -- so ``view.reshape(*batch,
+    rows, ld)`` gives the rows back (with the pad bytes past ``length``).
+    Returns ``(view, ld)``."""
+    if rows % group:
+        raise ValueError(f"row {'pairs' if group == 2 else 'quads'} need a row count divisible by {group}, got {rows}")
+    piece = 128 // group
+    ld = (length + piece - 1) // piece * piece
+    buf = torch.empty(tuple(batch) + (rows // group, ld // piece, group, piece), dtype=torch.uint8, device=device)
     return buf.transpose(-3, -2), ld
 
 
-def _pair_geometry(t: torch.Tensor, nbatch: int):
-    """``(rows, padded row bytes, ld)`` when ``t`` is a row-pair view with
-    ``nbatch`` leading batch dims (as ``_pair_buffer`` makes them), else
-    None (a row-major operand)."""
-    if t.dim() != nbatch + 4 or t.shape[-3] != 2 or t.shape[-1] != 64:
+def _pair_geometry(t: torch.Tensor, nbatch: int, group: int = 2):
+    """``(rows, padded row bytes, ld)`` when ``t`` is a row-group view of
+    ``group`` rows (2: pairs, 4: quads) with ``nbatch`` leading batch dims, as
+    ``_pair_buffer`` makes them, else None (a row-major operand)."""
+    piece = 128 // group
+    if t.dim() != nbatch + 4 or t.shape[-3] != group or t.shape[-1] != piece:
         return None
     st = t.stride()
-    if st[-1] != 1 or st[-3] != 64 or (t.shape[-2] > 1 and st[-2] != 128):
+    if st[-1] != 1 or st[-3] != piece or (t.shape[-2] > 1 and st[-2] != 128):
         return None
     if st[-4] % 128 or st[-4] < 128 * t.shape[-2]:
         return None
-    return 2 * t.shape[-4], 64 * t.shape[-2], st[-4] // 2
+    return group * t.shape[-4], piece * t.shape[-2], st[-4] // group
+
+
+def _to_row_groups(q: torch.Tensor, group: int) -> torch.Tensor:
+    *batch, R, L = q.shape
+    batch = tuple(batch)
+    view, ld = _pair_buffer(batch, R, L, q.device, group)
+    src = q.view(torch.uint8)
+    if ld != L:
+        padded = torch.zeros(batch + (R, ld), dtype=torch.uint8, device=q.device)
+        padded[..., :L] = src
+        src = padded
+    view.copy_(src.reshape(batch + (R // group, group, ld // (128 // group), 128 // group)))
+    return view.view(q.dtype)
 
 
 def to_row_pairs(q: torch.Tensor) -> torch.Tensor:
@@ -93,16 +110,18 @@ def to_row_pairs(q: torch.Tensor) -> torch.Tensor:
         raise ValueError("to_row_pairs expects (*batch, rows, length) data")
     if q.dtype != torch.float8_e4m3fn:
         raise TypeError(f"row pairs hold float8_e4m3fn data, got {q.dtype}")
-    *batch, R, L = q.shape
-    batch = tuple(batch)
-    view, ld = _pair_buffer(batch, R, L, q.device)
-    src = q.view(torch.uint8)
-    if ld != L:
-        padded = torch.zeros(batch + (R, ld), dtype=torch.uint8, device=q.device)
-        padded[..., :L] = src
-        src = padded
-    view.copy_(src.reshape(batch + (R // 2, 2, ld // 64, 64)))
-    return view.view(torch.float8_e4m3fn)
+    return _to_row_groups(q, 2)
+
+
+def to_row_quads(q: torch.Tensor) -> torch.Tensor:
+    """Row-quad copy of row-major packed e2m1 data ``(*batch, R, K/2)``
+    (R divisible by 4), the pad zero: what ``to_mx(..., elem_dtype=
+    torch.float4_e2m1fn_x2, data_layout="quads")`` writes."""
+    if q.dim() < 2:
+        raise ValueError("to_row_quads expects (*batch, rows, length) data")
+    if q.element_size() != 1 or q.dtype == torch.float8_e4m3fn:
+        raise TypeError(f"row quads hold packed e2m1 data (float4_e2m1fn_x2 or uint8), got {q.dtype}")
+    return _to_row_groups(q, 4)
 
 
 def _offsets(offs: torch.Tensor, device: torch.device) -> torch.Tensor:

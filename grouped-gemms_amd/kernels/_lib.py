@@ -30,8 +30,10 @@ DTYPE_F32 = 2
 SCALES_PLAIN = 0
 SCALES_STEPS = 1
 DATA_PAIRS = 2      # quantizer data outputs in row pairs (OR-ed into the scale layout)
+DATA_QUADS = 4      # quantizer packed e2m1 outputs in row quads
 A_PAIRS = 1         # *_steps GEMMs: A / go_t in row pairs
 B_PAIRS = 2         # *_steps GEMMs: B / ia_t in row pairs
+B_QUADS = 4         # mxgg_grouped_mm_steps: packed e2m1 B in row quads
 
 _c_i32 = ctypes.c_int
 _c_i64 = ctypes.c_int64

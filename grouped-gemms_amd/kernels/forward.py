@@ -17,8 +17,9 @@ scales may come step-major (int32 ``(T, M)`` and ``(E, T, N)``,
 the call then skips the re-layout launch (``mxgg_grouped_mm_steps``).  With
 step-major scales either e4m3 operand may also be in row pairs (the view
 ``(M/2, 2, cdiv(K, 64), 64)``, resp. ``(E, N/2, 2, cdiv(K, 64), 64)``, that
-``to_mx(..., data_layout="pairs")`` returns), which the kernels copy in whole
-128-byte lines.
+``to_mx(..., data_layout="pairs")`` returns), and a packed e2m1 weight in row
+quads (``(E, N/4, 4, cdiv(K/2, 32), 32)``, ``data_layout="quads"``), which the
+kernels copy in whole 128-byte lines.
 """
 
 from __future__ import annotations
@@ -110,20 +111,24 @@ def triton_mxfp8_grouped_mm(
         raise TypeError(f"input_act dtype {input_act.dtype} is not float8_e4m3fn")
     pa = _pair_geometry(input_act, 0)
     pb = _pair_geometry(weight, 1) if weight.dtype == torch.float8_e4m3fn else None
+    qb = _pair_geometry(weight, 1, 4) if weight.dtype in _FP4_DTYPES else None   # row quads
     M, Ka = (pa[0], pa[1]) if pa else input_act.shape
     if weight.dtype == torch.float8_e4m3fn:
         b_fmt = _lib.FMT_E4M3
         E, N, Kb = (weight.shape[0], pb[0], pb[1]) if pb else weight.shape
     elif weight.dtype in _FP4_DTYPES:
         b_fmt = _lib.FMT_E2M1
-        E, N, Kb = weight.shape[0], weight.shape[1], 2 * weight.shape[2]
+        E = weight.shape[0]
+        N, Kb = (qb[0], 2 * qb[1]) if qb else (weight.shape[1], 2 * weight.shape[2])
+        pb = qb
     else:
         raise TypeError(f"weight dtype {weight.dtype} is neither float8_e4m3fn nor packed fp4")
-    # K: the row-major operand's (row pairs round it up to 64)
+    # K: the row-major operand's (row pairs round it up to 64, quads of packed
+    # e2m1 likewise: 32 bytes)
     K = Kb if pa and not pb else Ka
-    pad = (pa or pb)[1] if (pa is None) != (pb is None) else None
-    if pad is not None:
-        assert (K + 63) // 64 * 64 == pad, f"K mismatch: {K} and row pairs of {pad} bytes"
+    if (pa is None) != (pb is None):
+        padded = Ka if pa else Kb
+        assert (K + 63) // 64 * 64 == padded, f"K mismatch: {K} and a row-group operand spanning {padded}"
     else:
         assert Ka == Kb, f"K mismatch: A={Ka}, B={Kb}" + (" (packed fp4: K/2 bytes)" if b_fmt else "")
     if K % 32:
@@ -131,7 +136,7 @@ def triton_mxfp8_grouped_mm(
     steps = input_act_scales.dtype == torch.int32
     if steps != (weight_scales.dtype == torch.int32):
         raise TypeError("input_act_scales and weight_scales must both be e8m0 bytes or both step-major int32")
-    layout = (_lib.A_PAIRS if pa else 0) | (_lib.B_PAIRS if pb else 0)
+    layout = (_lib.A_PAIRS if pa else 0) | ((_lib.B_QUADS if qb else _lib.B_PAIRS) if pb else 0)
     if layout and not steps:
         raise TypeError("row-pair operands need step-major int32 scales (scale_layout='steps')")
     T = (K + 127) // 128

@@ -23,9 +23,11 @@ and 2i+1 interleaved in 64-byte pieces, returned as the strided view
 ``(*batch, R/2, 2, cdiv(L, 64), 64)`` (``_common._pair_buffer``; the pad
 bytes past L are zero).  The GEMMs stage a 64-element slice of two adjacent
 rows per step, which is then one 128-byte line instead of halves of two:
-13% less time for the forward and 20% for the weight gradient over the
-benchmark shapes, same bits.  The GEMM wrappers recognise such views (with
-step-major scales).
+13% less time for the forward and 19% for the weight gradient over the
+benchmark shapes, same bits.  Packed e2m1 (32 bytes per 64-element step of a
+row) goes in row quads the same way (``data_layout="quads"``, the view
+``(*batch, R/4, 4, cdiv(L/2, 32), 32)``).  The GEMM wrappers recognise such
+views (with step-major scales).
 """
 
 from __future__ import annotations
@@ -54,12 +56,11 @@ def _layout_code(scale_layout: str) -> int:
     raise ValueError(f"scale_layout must be 'plain' or 'steps', got {scale_layout!r}")
 
 
-def _pairs_flag(data_layout: str) -> bool:
-    if data_layout == "rows":
-        return False
-    if data_layout == "pairs":
-        return True
-    raise ValueError(f"data_layout must be 'rows' or 'pairs', got {data_layout!r}")
+def _pairs_flag(data_layout: str, allowed=("rows", "pairs")) -> bool:
+    """True for a row-group layout ("pairs" / "quads"), False for "rows"."""
+    if data_layout not in allowed:
+        raise ValueError(f"data_layout must be one of {allowed}, got {data_layout!r}")
+    return data_layout != "rows"
 
 
 def _aligned_rows(batch: tuple, rows: int, length: int, device) -> tuple:
@@ -92,7 +93,9 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
     ``scale_layout="steps"`` the scales are step-major int32
     ``(*data.shape[:-2], cdiv(L, 128), data.shape[-2])`` instead.
     ``data_layout="pairs"`` (e4m3, ``data.shape[-2]`` even): ``data_q`` in
-    row pairs, the view ``(*data.shape[:-2], R/2, 2, cdiv(L, 64), 64)``.
+    row pairs, the view ``(*data.shape[:-2], R/2, 2, cdiv(L, 64), 64)``;
+    ``data_layout="quads"`` (e2m1, ``data.shape[-2]`` divisible by 4): in row
+    quads, the view ``(*data.shape[:-2], R/4, 4, cdiv(L/2, 32), 32)``.
     """
     fp4 = _FP4 is not None and elem_dtype is _FP4
     assert elem_dtype is torch.float8_e4m3fn or fp4, "only e4m3fn and e2m1fn_x2 supported"
@@ -110,11 +113,11 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
     rows = x.shape[0]
     qcols = L // 2 if fp4 else L
     lay = _layout_code(scale_layout)
-    pairs = _pairs_flag(data_layout)
+    pairs = _pairs_flag(data_layout, ("rows", "pairs", "quads"))
     if pairs:
-        if fp4 or len(shape) < 2:
-            raise ValueError("data_layout='pairs' needs e4m3 output and at least 2 dims")
-        qv, ld_q = _pair_buffer(shape[:-2], shape[-2], L, data.device)
+        if data_layout != ("quads" if fp4 else "pairs") or len(shape) < 2:
+            raise ValueError("data_layout 'pairs' holds e4m3 output and 'quads' packed e2m1, with at least 2 dims")
+        qv, ld_q = _pair_buffer(shape[:-2], shape[-2], qcols, data.device, 4 if fp4 else 2)
         q_ptr = qv.data_ptr()
     else:
         q = torch.empty((rows, qcols), dtype=torch.uint8, device=data.device)
@@ -129,11 +132,12 @@ def to_mx(data: torch.Tensor, elem_dtype=torch.float8_e4m3fn, block_size: int = 
     lib = _lib.load()
     rc = lib.mxgg_quantize_mx(x.data_ptr(), code, rows, L, x.stride(0) if rows > 1 else L,
                               _lib.FMT_E2M1 if fp4 else _lib.FMT_E4M3,
-                              q_ptr, ld_q, s.data_ptr(), ld_s, lay | (_lib.DATA_PAIRS if pairs else 0),
+                              q_ptr, ld_q, s.data_ptr(), ld_s,
+                              lay | ((_lib.DATA_QUADS if fp4 else _lib.DATA_PAIRS) if pairs else 0),
                               _stream_handle(data.device))
     _lib.check(rc)
     if pairs:
-        q = qv.view(torch.float8_e4m3fn)
+        q = qv.view(_FP4 if fp4 else torch.float8_e4m3fn)
     else:
         q = q.view(_FP4 if fp4 else torch.float8_e4m3fn).reshape(shape[:-1] + (qcols,))
     if lay == _lib.SCALES_STEPS:

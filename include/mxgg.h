@@ -40,7 +40,11 @@
  * GEMM stages per step is one 128-byte line (row-major, each is half of two
  * lines).  Bytes L .. L rounded up to 64 of a row are padding, which the
  * GEMMs do not read (they take the true K, resp. M); the quantizers write
- * zeros there.
+ * zeros there.  Row quads (MXGG_DATA_QUADS, MXGG_B_QUADS) are the same for
+ * packed e2m1 data, whose 64-element stage piece of a row is 32 bytes: 4 rows
+ * (R divisible by 4) interleave in 32-byte pieces, byte k of row r at
+ * (r/4)*4*ld + (k/32)*128 + (r%4)*32 + k%32, ld = the row's bytes rounded up
+ * to 32.
  */
 #ifndef MXGG_H_
 #define MXGG_H_
@@ -75,11 +79,13 @@ extern "C" {
 #define MXGG_SCALES_PLAIN 0   /* (rows, nblk) bytes, row stride ld_s */
 #define MXGG_SCALES_STEPS 1   /* step-major dwords (see above); ld_s = R, the rows per batch */
 #define MXGG_DATA_PAIRS 2     /* e4m3 data outputs in row pairs (see above) */
+#define MXGG_DATA_QUADS 4     /* packed e2m1 data outputs in row quads (see above) */
 
 /* operand layouts of mxgg_grouped_mm_steps / mxgg_wgrad_steps (bit flags;
  * 0 = both row-major) */
 #define MXGG_A_PAIRS 1   /* A (forward) or go_t (wgrad) in row pairs */
 #define MXGG_B_PAIRS 2   /* B (forward; e4m3 only) or ia_t (wgrad) in row pairs */
+#define MXGG_B_QUADS 4   /* B (forward; packed e2m1 only) in row quads */
 
 /* Library version (MXGG_VERSION of the build). */
 int mxgg_version(void);
@@ -103,7 +109,9 @@ int mxgg_device_supported(void);
  *              (ld_s divides rows; e.g. ld_s = N for an (E, N, K) weight
  *              given as E*N rows), 4 * rows * ceil(cols/128) bytes.
  *   scale_layout | MXGG_DATA_PAIRS: q in row pairs (E4M3, rows even, ld_q a
- *              multiple of 64 and at least cols rounded up to 64).
+ *              multiple of 64 and at least cols rounded up to 64);
+ *              | MXGG_DATA_QUADS: q in row quads (E2M1, rows divisible by 4,
+ *              ld_q a multiple of 32 and at least cols/2 rounded up to 32).
  * cols must be a multiple of 32.
  */
 int mxgg_quantize_mx(const void* src, int src_dtype, int64_t rows, int64_t cols,
@@ -235,7 +243,8 @@ int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t l
  * reference pre-shuffles its scales on every call too, kernels/forward.py:
  * 367-397, 528-550).  layout: MXGG_A_PAIRS and / or MXGG_B_PAIRS for operands
  * in row pairs (lda, ldb_n then at least K rounded up to 64; M, resp. N,
- * even).  workspace / ws_bytes (may be null / 0): room for
+ * even), MXGG_B_QUADS for a packed e2m1 B in row quads (ldb_n at least K/2
+ * rounded up to 32, N divisible by 4).  workspace / ws_bytes (may be null / 0): room for
  * the fp32 partial tiles of a split last round;
  * mxgg_grouped_mm_workspace_size() is always enough.  Results are
  * bit-identical to mxgg_grouped_mm given a workspace with the same room after

@@ -165,16 +165,17 @@ def test_wgrad_and_quant_validation_without_gpu():
 
 
 def test_row_pair_argument_checks():
-    """Row-pair operands (MXGG_DATA_PAIRS / MXGG_A_PAIRS / MXGG_B_PAIRS) are
-    checked before anything launches: even row counts, strides that hold
-    the rows rounded up to 64 bytes, e4m3 only, known flags."""
+    """Row-pair and row-quad operands (MXGG_DATA_PAIRS / _QUADS, MXGG_A_PAIRS /
+    MXGG_B_PAIRS / MXGG_B_QUADS) are checked before anything launches: row
+    counts divisible by 2 (4), strides that hold the rows rounded up to the
+    64 (32) byte piece, e4m3 (packed e2m1) only, known flags."""
     from kernels import _lib
     lib = _lib.load()
     P, S = _lib.DATA_PAIRS, _lib.SCALES_STEPS
     err = lib.mxgg_last_error_string
     # quantizers: rows must pair up; the stride a multiple of 64 holding the padded row; e4m3 only
     rc = lib.mxgg_quantize_mx(16, 0, 5, 64, 64, 0, 16, 64, 16, 2, P, None)
-    assert rc == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert rc == _lib.ERR_INVALID_ARG and b"divisible by 2" in err()
     rc = lib.mxgg_quantize_mx(16, 0, 6, 96, 96, 0, 16, 112, 16, 3, P, None)
     assert rc == _lib.ERR_INVALID_ARG and b"multiple of 64" in err()
     rc = lib.mxgg_quantize_mx(16, 0, 6, 96, 96, 0, 16, 96, 16, 3, P, None)
@@ -189,19 +190,36 @@ def test_row_pair_argument_checks():
     # forward: known flags; e4m3 weights only; M / N even; strides hold K rounded up to 64
     fwd = lambda M, N, K, lda, ldb, fmt, layout: lib.mxgg_grouped_mm_steps(
         16, lda, 16, 16, fmt, ldb, N * ldb, 16, 16, 1, M, N, K, 16, 0, N, 0, 0, 0, 0, layout, None, 0, None)
-    assert fwd(64, 64, 64, 64, 64, 0, 4) == _lib.ERR_INVALID_ARG and b"layout flags" in err()
+    assert fwd(64, 64, 64, 64, 64, 0, 8) == _lib.ERR_INVALID_ARG and b"layout flags" in err()
     assert fwd(64, 64, 64, 64, 32, _lib.FMT_E2M1, _lib.B_PAIRS) == _lib.ERR_UNSUPPORTED
-    assert fwd(63, 64, 64, 64, 64, 0, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
-    assert fwd(64, 65, 64, 64, 64, 0, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert fwd(63, 64, 64, 64, 64, 0, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"divisible by 2" in err()
+    assert fwd(64, 65, 64, 64, 64, 0, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"divisible by 2" in err()
     assert fwd(63, 65, 64, 64, 64, 0, 0) != _lib.ERR_INVALID_ARG       # odd counts are fine row-major
     assert fwd(64, 64, 96, 112, 128, 0, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
     assert fwd(64, 64, 96, 128, 112, 0, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
+    # row quads: packed e2m1 weights only, N divisible by 4, stride holding K/2 rounded up to 32
+    Q = _lib.DATA_QUADS
+    assert fwd(64, 64, 64, 64, 64, 0, _lib.B_QUADS) == _lib.ERR_UNSUPPORTED
+    assert fwd(64, 64, 64, 64, 32, _lib.FMT_E2M1, _lib.B_QUADS | _lib.B_PAIRS) == _lib.ERR_INVALID_ARG
+    assert fwd(64, 66, 64, 64, 32, _lib.FMT_E2M1, _lib.B_QUADS) == _lib.ERR_INVALID_ARG and b"divisible by" in err()
+    assert fwd(64, 64, 96, 128, 48, _lib.FMT_E2M1, _lib.B_QUADS) == _lib.ERR_INVALID_ARG and b"stride" in err()
+    assert fwd(64, 68, 96, 128, 64, _lib.FMT_E2M1, _lib.B_QUADS) != _lib.ERR_INVALID_ARG
+    rc = lib.mxgg_quantize_mx(16, 0, 8, 64, 64, 0, 16, 64, 16, 2, Q, None)
+    assert rc == _lib.ERR_UNSUPPORTED                              # quads hold e2m1, not e4m3
+    rc = lib.mxgg_quantize_mx(16, 0, 6, 64, 64, _lib.FMT_E2M1, 16, 32, 16, 2, Q, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"divisible by 4" in err()
+    rc = lib.mxgg_quantize_mx(16, 0, 8, 96, 96, _lib.FMT_E2M1, 16, 48, 16, 3, Q, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"multiple of 32 and holds 64 bytes" in err()
+    assert lib.mxgg_quantize_mx(16, 0, 8, 96, 96, _lib.FMT_E2M1, 16, 64, 16, 3, Q, None) != _lib.ERR_INVALID_ARG
+    assert lib.mxgg_quantize_mx(16, 0, 8, 64, 64, 0, 16, 64, 16, 2, P | Q, None) == _lib.ERR_INVALID_ARG
+    assert lib.mxgg_quantize_mx_dim0(16, 0, 64, 64, 64, 0, 16, 64, 16, 64, Q | S, None) == _lib.ERR_UNSUPPORTED
     # wgrad: the same for go_t (A_PAIRS) and ia_t (B_PAIRS) along the tokens
     wg = lambda M, N, K, ldg, ldi, layout: lib.mxgg_wgrad_steps(
         16, ldg, 16, 16, ldi, 16, 16, 1, M, N, K, 16, 0, layout, None, 0, None)
     assert wg(96, 64, 64, 128, 128, 8) == _lib.ERR_INVALID_ARG and b"layout flags" in err()
     assert wg(96, 63, 64, 128, 128, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
     assert wg(96, 64, 65, 128, 128, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"even row count" in err()
+    assert wg(96, 64, 64, 128, 128, _lib.B_QUADS) == _lib.ERR_INVALID_ARG and b"layout flags" in err()
     assert wg(96, 64, 64, 112, 128, _lib.A_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
     assert wg(96, 64, 64, 128, 112, _lib.B_PAIRS) == _lib.ERR_INVALID_ARG and b"stride" in err()
 

@@ -1,18 +1,22 @@
 """Row-pair operands (``data_layout="pairs"`` / ``MXGG_DATA_PAIRS``,
 ``MXGG_A_PAIRS`` / ``MXGG_B_PAIRS``): rows 2i and 2i+1 interleaved in 64-byte
-pieces, so the GEMMs copy whole 128-byte lines.  A layout of this build with
-no counterpart in the reference, held to the row-major path bit for bit:
+pieces, so the GEMMs copy whole 128-byte lines; and row quads of packed e2m1
+weights (``data_layout="quads"``, ``MXGG_B_QUADS``: 4 rows in 32-byte
+pieces).  A layout of this build with no counterpart in the reference, held
+to the row-major path bit for bit:
 
 * the quantizers' row-pair output holds the bytes of their row-major output
   (read back through the returned view, and at the byte offsets the C header
   documents, on the raw storage), the pad past an odd multiple of 32 is
   zero, and the scales are unchanged;
-* ``to_row_pairs`` of row-major data equals the quantizers' row-pair output;
+* ``to_row_pairs`` / ``to_row_quads`` of row-major data equal the quantizers'
+  row-group output;
 * the forward / dgrad and wgrad GEMMs return the same bits with either
   operand, or both, in row pairs as with both row-major: group starts at odd
   rows (a tile whose first row is the second of a pair), partial tiles,
   128 x 128 tiles, split launches and (among the benchmark shapes)
-  quarter-tile ones, f32 / f16 outputs, an e2m1 weight beside a row-pair A,
+  quarter-tile ones, f32 / f16 outputs, an e2m1 weight row-major or in row
+  quads beside a row-major or row-pair A (BASELINE config 5 at full size),
   token ranges off the 16 grid (the wgrad's edge chunks), 2080 tokens (rows
   padded to 2112), and every benchmark shape.
 """
@@ -76,6 +80,32 @@ def test_to_mx_pairs_holds_the_rows(gpu, dtype, shape):
                        _u8(q_p).reshape(rows.shape[:-1] + (-1,)))
 
 
+@pytest.mark.parametrize("shape", [(96, 544), (3, 40, 96), (8, 128), (2080, 96)])
+def test_to_mx_e2m1_quads_hold_the_rows(gpu, shape):
+    import kernels
+    from kernels._common import to_row_quads
+    fp4 = torch.float4_e2m1fn_x2
+    x = _x(shape, sum(shape) + 3, gpu, 3.0)
+    s_r, q_r = kernels.to_mx(x, elem_dtype=fp4, scale_layout="steps")
+    s_q, q_q = kernels.to_mx(x, elem_dtype=fp4, scale_layout="steps", data_layout="quads")
+    Lb = shape[-1] // 2
+    assert q_q.dtype == fp4
+    assert tuple(q_q.shape) == shape[:-2] + (shape[-2] // 4, 4, -(-Lb // 32), 32)
+    assert torch.equal(s_q, s_r)
+    *b, G, four, S, P = q_q.shape
+    r = _u8(q_q).reshape(tuple(b) + (4 * G, 32 * S))
+    assert torch.equal(r[..., :Lb], _u8(q_r))
+    assert not r[..., Lb:].any()
+    assert torch.equal(_u8(to_row_quads(q_r)).reshape(r.shape), r)
+    # byte k of row r at (r/4) 4 ld + (k/32) 128 + (r%4) 32 + k%32 of the storage
+    if len(shape) == 2:
+        R, ld = shape[0], 32 * S
+        flat = torch.as_strided(_u8(q_q), (R * ld,), (1,)).cpu().numpy()
+        rr, kk = np.meshgrid(np.arange(R), np.arange(Lb), indexing="ij")
+        np.testing.assert_array_equal(flat[(rr // 4) * 4 * ld + (kk // 32) * 128 + (rr % 4) * 32 + kk % 32],
+                                      _u8(q_r).cpu().numpy())
+
+
 def test_pair_storage_matches_documented_offsets(gpu):
     """Byte k of row r at (r/2) 2 ld + (k/64) 128 + (r%2) 64 + k%64 of the
     storage (the formula of include/mxgg.h), pad bytes zero."""
@@ -120,6 +150,10 @@ def test_pairs_need_e4m3_and_even_rows(gpu):
     with pytest.raises(ValueError):
         kernels.to_mx(_x((4, 64), 1, gpu), elem_dtype=torch.float4_e2m1fn_x2, data_layout="pairs")
     with pytest.raises(ValueError):
+        kernels.to_mx(_x((4, 64), 1, gpu), data_layout="quads")
+    with pytest.raises(ValueError):
+        kernels.to_mx(_x((6, 64), 1, gpu), elem_dtype=torch.float4_e2m1fn_x2, data_layout="quads")
+    with pytest.raises(ValueError):
         kernels.to_mx(_x((4, 64), 1, gpu), data_layout="cols")
 
 
@@ -142,7 +176,12 @@ def _fwd_all_layouts(gpu, E, M, N, K, offs, seed, out_dtype=torch.bfloat16, fp4=
     ref = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, o, out_dtype=out_dtype)[:rows]
     pa = to_row_pairs(qa)
     cases = {"A pairs": (pa, qw)}
-    if not fp4:
+    if fp4:
+        from kernels._common import to_row_quads
+        _, qq = kernels.to_mx(w, elem_dtype=fp, scale_layout="steps", data_layout="quads")
+        assert torch.equal(_u8(to_row_quads(qw)).reshape(-1), _u8(qq).reshape(-1))
+        cases.update({"B quads": (qa, qq), "both": (pa, qq)})
+    else:
         pw = to_row_pairs(qw)
         cases.update({"B pairs": (qa, pw), "both": (pa, pw)})
     for what, (x_, w_) in cases.items():
@@ -173,6 +212,14 @@ def test_fwd_pairs_other_outputs(gpu, out_dtype):
 
 def test_fwd_pairs_beside_e2m1_weight(gpu):
     _fwd_all_layouts(gpu, 4, 2048, 512, 1024, _odd_offs(4, 2048, 3), seed=11, fp4=True)
+    _fwd_all_layouts(gpu, 3, 1000, 324, 1056, _odd_offs(3, 1000, 5), seed=12, fp4=True)   # K/2 % 32 == 16, N % 256
+
+
+def test_fwd_e2m1_quads_config5(gpu):
+    """BASELINE config 5 (e4m3 x e2m1, E=8, M=16640, N=8192, K=5120) at full size."""
+    import random
+    offs = O.generate_jagged_offs(8, M_TOKENS, 32, rng=random.Random(4))
+    _fwd_all_layouts(gpu, 8, M_TOKENS, 8192, 5120, offs, seed=5, fp4=True)
 
 
 def test_fwd_pairs_need_step_scales(gpu):
