@@ -114,6 +114,31 @@ def test_fwd_rows_past_last_offset_untouched(gpu):
     _assert_close(f32(out), ref, rows=320)
 
 
+def test_fwd_empty_reduction_gives_zeros(gpu):
+    """K = 0 through the C ABI, on an output pre-filled with NaN: every routed
+    row becomes zero (the ring runs one stage wholly outside the reduction,
+    whose MFMAs start the accumulators from zero), rows past offs[-1] stay."""
+    from kernels import _lib
+    lib = _lib.load()
+    M, N, E = 96, 64, 2
+    dummy = torch.zeros(4096, dtype=torch.uint8, device=gpu)   # holds every row range the calls name
+    offs = torch.tensor([40, 80], dtype=torch.int32, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    for steps in (False, True):
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        p = dummy.data_ptr()
+        if steps:
+            rc = lib.mxgg_grouped_mm_steps(p, 16, p, p, 0, 16, 16 * N, p, offs.data_ptr(), E, M, N, 0,
+                                           out.data_ptr(), 0, N, 0, 0, 0, 0, 0, None, 0, stream)
+        else:
+            rc = lib.mxgg_grouped_mm(p, 16, p, 1, p, 0, 16, 16 * N, p, 1, N, offs.data_ptr(), E, M, N, 0,
+                                     out.data_ptr(), 0, N, 0, 0, 0, 0, None, 0, stream)
+        _lib.check(rc)
+        torch.cuda.synchronize()
+        assert not out[:80].float().abs().sum().item(), f"steps={steps}"
+        assert out[80:].float().isnan().all(), f"steps={steps}"
+
+
 @pytest.mark.parametrize("N,K", [(200, 96), (33, 160), (4096, 32)])
 def test_fwd_odd_shapes(gpu, N, K):
     """N not a multiple of the tile / of 4, K not a multiple of 128 (masked tail)."""
