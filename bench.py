@@ -119,6 +119,25 @@ def read_traffic(kernel: str):
     return None
 
 
+def read_trace_avg(kernel: str, native: bool):
+    """(calls, average µs) of `kernel`'s kernel-only calls in the committed
+    kernel-trace summary (profiles/kernel_stats_sweep.txt: the span of each
+    call's GEMM dispatches, the sweep's first cold calls, or the native
+    sweep's after them), or None when the summary lacks that kernel."""
+    path = os.path.join(ROOT, "profiles", "kernel_stats_sweep.txt")
+    if not os.path.exists(path):
+        return None
+    pat = (r"the native sweep's (\d+) after them: avg\s+([\d.]+) us" if native
+           else r"the sweep's first (\d+): avg\s+([\d.]+) us")
+    for line in open(path):
+        head = line.strip().split("all calls")[0].strip()
+        if head and canon(head) == canon(kernel):
+            m = re.search(pat, line)
+            if m:
+                return int(m.group(1)), float(m.group(2))
+    return None
+
+
 def copy_calibration(dev, mib: int = 256, reps: int = 3):
     """A plain device copy of known size, run so that a PMC pass over this
     program can scale FETCH_SIZE / WRITE_SIZE (the copy moves mib MiB each way)."""
@@ -394,17 +413,29 @@ def make_roofline(stats, tag, scope):
     time over the timed reps): algorithmic FLOPs 2*M*N*K per call / the mean
     time of the call's GEMM launches (HIP events on the launch stream; the
     split / quarter-tile tails included).  tag: suffix of the kernel's entry
-    in the committed HBM-traffic summary."""
+    in the committed HBM-traffic summary.  Beside it, `profile`: the same
+    FLOPs over the mean per-call span the committed kernel-trace summary
+    records for those calls (rocprofv3 durations of a profiled run of this
+    bench), when it has them."""
     if not stats:
         return None
     kname, k = max(stats.items(), key=lambda kv: kv[1]["ms"])
     achieved = k["flops"] / (k["ms"] * 1e-3) / 1e12
+    prof = None
+    tr = read_trace_avg(kname, bool(tag))
+    if tr:
+        p_ach = k["flops"] / k["launches"] / (tr[1] * 1e-6) / 1e12
+        prof = {"avg_launch_us": tr[1], "calls": tr[0], "achieved": round(p_ach, 1),
+                "frac": round(p_ach / PEAK_MXFP8_TFLOPS, 4),
+                "source": "profiles/kernel_stats_sweep.txt: rocprofv3 kernel-trace spans of the same calls in a "
+                          "profiled run of this bench (this run's FLOPs per call)"}
     return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MXFP8_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_MXFP8_TFLOPS, 4),
             "traffic": read_traffic(kname + tag), "kernel": kname, "scope": scope,
             "avg_launch_us": round(k["ms"] / k["launches"] * 1e3, 2),
             "flops_per_launch": round(k["flops"] / k["launches"]),
             "launches": k["launches"],
+            "profile": prof,
             "by_kernel": {n: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 2),
                               "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
                               "launches": v["launches"]} for n, v in stats.items()}}
