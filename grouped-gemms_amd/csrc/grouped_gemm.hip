@@ -473,8 +473,12 @@ __device__ __forceinline__ void interleave_step() {
 // (Fn, xn, wn), start the copies of stage s0 + r + NS and, when stage
 // s0 + r + 1 opens a scale group, the scales of the group after it.
 // (s0 is the ring's first stage, even, in slot 0; t0 = s0 / 2 its step.)
-// FIRST: stage s0, whose MFMAs start the accumulators from zero.
-template <class C, bool FIRST = false>
+// FIRST: stage s0, whose MFMAs start the accumulators from zero.  TAIL:
+// kStageFull as described; kStageNoCopy, the last stage but one, starts no
+// copies (any would fetch a stage past the run: zero fills that only load the
+// LDS port); kStageLast, the last stage, only multiplies.
+constexpr int kStageFull = 0, kStageNoCopy = 1, kStageLast = 2;
+template <class C, bool FIRST = false, int TAIL = kStageFull>
 __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, const Operand& W,
                                            __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P, int s0, int r,
                                            int lo, int hi, Frags<C>& Fc, uint32_t (&xc)[C::FM],
@@ -487,6 +491,12 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   uint8_t* cur = smem + (r % C::NS) * C::STAGE;
   const uint8_t* nxt = smem + (rn % C::NS) * C::STAGE;
   const uint8_t* snx = smem + C::SOFF + ((rn / SPG) & 1) * C::SSLOT;
+  if constexpr (TAIL == kStageLast) {
+    mfma_range<C, 0, NMMA, FIRST>(Fc, xc, wc, acc);
+    hold(Fc, xc, wc);
+    MXGG_SCHED_FENCE();
+    return;
+  }
   mfma_range<C, 0, NE, FIRST>(Fc, xc, wc, acc);
   MXGG_SCHED_FENCE();
   MXGG_WAIT_VM((C::NS - 2) * C::LPS);       // this wave's copies of stage r+1 have landed
@@ -500,12 +510,14 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   // (last read, of stage r, before this barrier): group g+1 goes there
   // (a group that starts past the reduction range is never read: not copied,
   // so the drain after the last stage waits for no memory read)
-  const int tg = s0 / 2 + (rn / SPG + 1) * SCG;
-  const bool opens = rn % SPG == 0 && tg * STEP < hi;
-  issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, ssr, P, tg, opens);
-  issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
+  if constexpr (TAIL == kStageFull) {
+    const int tg = s0 / 2 + (rn / SPG + 1) * SCG;
+    const bool opens = rn % SPG == 0 && tg * STEP < hi;
+    issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, ssr, P, tg, opens);
+    issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
+  }
   mfma_range<C, NE, NMMA, FIRST>(Fc, xc, wc, acc);
-  interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, C::LPS>();
+  interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, TAIL == kStageFull ? C::LPS : 0>();
   MXGG_SCHED_FENCE();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   finish_scales<C>(xn, wn, s0 + rn, lo, hi);
@@ -556,16 +568,25 @@ __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, c
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   finish_scales<C>(xa, wa, s0, lo, hi);
   const int n = s1 - s0;
-  int r0 = 0;
   if constexpr (ZSTART) {
+    // stages run: n rounded up to even, at least 4 (those past s1 hold zeros);
+    // the last two start no copies, the last reads nothing
+    const int nr = n < 4 ? 4 : (n + 1) & ~1;
     ring_stage<C, true>(smem, X, W, ssr, P, s0, 0, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
     ring_stage<C>(smem, X, W, ssr, P, s0, 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
-    r0 = 2;
-  }
 #pragma nounroll
-  for (int r = r0; r < n; r += 2) {
-    ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-    ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    for (int r = 2; r < nr - 2; r += 2) {
+      ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+      ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    }
+    ring_stage<C, false, kStageNoCopy>(smem, X, W, ssr, P, s0, nr - 2, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+    ring_stage<C, false, kStageLast>(smem, X, W, ssr, P, s0, nr - 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+  } else {
+#pragma nounroll
+    for (int r = 0; r < n; r += 2) {
+      ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+      ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    }
   }
   // copies past the last stage (zero fills, scale groups) may still be
   // writing LDS: drain them before the LDS is reused or released
