@@ -474,10 +474,12 @@ __device__ __forceinline__ void interleave_step() {
 // s0 + r + 1 opens a scale group, the scales of the group after it.
 // (s0 is the ring's first stage, even, in slot 0; t0 = s0 / 2 its step.)
 // FIRST: stage s0, whose MFMAs start the accumulators from zero.  TAIL:
-// kStageFull as described; kStageNoCopy, the last stage but one, starts no
-// copies (any would fetch a stage past the run: zero fills that only load the
-// LDS port); kStageLast, the last stage, only multiplies.
-constexpr int kStageFull = 0, kStageNoCopy = 1, kStageLast = 2;
+// kStageFull as described; kStageNoCopy2 / 1 / 0, the fourth, third and
+// second stage from the end, start no copies (any would fetch a stage past the
+// run: zero fills that only load the LDS port), so the wait for the next
+// stage allows for the copies of 2 / 1 / 0 later stages only; kStageLast,
+// the last stage, only multiplies.
+constexpr int kStageFull = 0, kStageNoCopy2 = 1, kStageNoCopy1 = 2, kStageNoCopy0 = 3, kStageLast = 4;
 template <class C, bool FIRST = false, int TAIL = kStageFull>
 __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, const Operand& W,
                                            __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P, int s0, int r,
@@ -499,7 +501,14 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   }
   mfma_range<C, 0, NE, FIRST>(Fc, xc, wc, acc);
   MXGG_SCHED_FENCE();
-  MXGG_WAIT_VM((C::NS - 2) * C::LPS);       // this wave's copies of stage r+1 have landed
+  // this wave's copies of stage r+1 have landed (the copies of the NS-2
+  // stages after it may still be in flight; in the tail, of those issued)
+  if constexpr (TAIL == kStageNoCopy1)
+    MXGG_WAIT_VM(C::LPS);
+  else if constexpr (TAIL == kStageNoCopy0)
+    MXGG_WAIT_VM(0);
+  else
+    MXGG_WAIT_VM((C::NS - 2) * C::LPS);
   MXGG_BARRIER();                           // ... every wave's; and stage r's slot is free
   MXGG_SCHED_FENCE();
   // LDS reads first, then the copies: a read issued after an LDS-DMA load
@@ -518,6 +527,7 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   }
   mfma_range<C, NE, NMMA, FIRST>(Fc, xc, wc, acc);
   interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, TAIL == kStageFull ? C::LPS : 0>();
+  static_assert(C::NS == 4, "the tail stages assume a 4-deep ring");
   MXGG_SCHED_FENCE();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   finish_scales<C>(xn, wn, s0 + rn, lo, hi);
@@ -569,17 +579,20 @@ __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, c
   finish_scales<C>(xa, wa, s0, lo, hi);
   const int n = s1 - s0;
   if constexpr (ZSTART) {
-    // stages run: n rounded up to even, at least 4 (those past s1 hold zeros);
-    // the last two start no copies, the last reads nothing
-    const int nr = n < 4 ? 4 : (n + 1) & ~1;
+    // stages run: n rounded up to even, at least 6 (those past s1 hold
+    // zeros); the last four start no copies (the prologue and the full
+    // stages already issued every stage of the run), the last reads nothing
+    const int nr = n < 6 ? 6 : (n + 1) & ~1;
     ring_stage<C, true>(smem, X, W, ssr, P, s0, 0, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
     ring_stage<C>(smem, X, W, ssr, P, s0, 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
 #pragma nounroll
-    for (int r = 2; r < nr - 2; r += 2) {
+    for (int r = 2; r < nr - 4; r += 2) {
       ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
       ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
     }
-    ring_stage<C, false, kStageNoCopy>(smem, X, W, ssr, P, s0, nr - 2, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+    ring_stage<C, false, kStageNoCopy2>(smem, X, W, ssr, P, s0, nr - 4, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+    ring_stage<C, false, kStageNoCopy1>(smem, X, W, ssr, P, s0, nr - 3, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    ring_stage<C, false, kStageNoCopy0>(smem, X, W, ssr, P, s0, nr - 2, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
     ring_stage<C, false, kStageLast>(smem, X, W, ssr, P, s0, nr - 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
   } else {
 #pragma nounroll
