@@ -908,10 +908,39 @@ struct ScaleJob {
   int tiles_r; int tiles_t;      // 64-row x 16-step tiles per batch
 };
 
+// An e4m3 operand copied from rows into row pairs (the layout the GEMM
+// copies in whole 128-byte lines): `batches` blocks of `rows` rows (even) of
+// `len` bytes, row r of batch b at src + b * ld_b + r * ld_r (16-byte
+// aligned); byte k of row r of batch b goes to dst + b * rows * ld_dst +
+// (r / 2) * 2 * ld_dst + (k / 64) * 128 + (r % 2) * 64 + k % 64, ld_dst =
+// len rounded up to 64, bytes past len zero.
+struct PairJob {
+  const uint8_t* src; int64_t ld_r; int64_t ld_b;
+  uint8_t* dst; int ld_dst; int pairs; int batches; int len;   // pairs = rows / 2
+};
+
 struct ScaleJobs {
   ScaleJob j[2];
   int tiles0;                    // workgroups of job 0 (job 1 follows)
+  int tiles01;                   // workgroups of jobs 0 and 1 (the pair job follows)
+  PairJob d;
 };
+
+// Pair job, workgroup w: row pair q of batch b (w = b * pairs + q), its
+// 2 * ld_dst output bytes in 16-byte chunks, consecutive threads on
+// consecutive chunks (coalesced stores; four threads read one 64-byte row
+// piece).  The source is read once: non-temporal loads.
+__device__ __forceinline__ void pair_chunks(const PairJob& J, int w) {
+  const int b = w / J.pairs, q = w - b * J.pairs;
+  const uint8_t* src = J.src + b * J.ld_b + (int64_t)(2 * q) * J.ld_r;
+  uint8_t* dst = J.dst + ((int64_t)b * J.pairs + q) * 2 * J.ld_dst;
+  for (int o = 16 * (int)threadIdx.x; o < 2 * J.ld_dst; o += 16 * 256) {
+    const int h = (o >> 6) & 1, k = (o >> 7) * 64 + (o & 63);
+    v4i v = {0, 0, 0, 0};
+    if (k < J.len) v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src + h * J.ld_r + k));
+    *reinterpret_cast<v4i*>(dst + o) = v;
+  }
+}
 
 // 64 rows x 16 steps per workgroup (256 threads): each thread reads 16
 // source bytes of one row (4 steps; one 16-byte load when the chunk is
@@ -921,6 +950,10 @@ struct ScaleJobs {
 __global__ __launch_bounds__(256) void scale_relayout_kernel(ScaleJobs js) {
   __shared__ uint32_t tile[16][65];
   int bid = blockIdx.x;
+  if (bid >= js.tiles01) {
+    pair_chunks(js.d, bid - js.tiles01);
+    return;
+  }
   const int which = bid < js.tiles0 ? 0 : 1;
   const ScaleJob& J = js.j[which];
   if (which) bid -= js.tiles0;
@@ -1793,13 +1826,19 @@ ScaleJob scale_job(const uint8_t* src, int64_t ld_r, int64_t ld_b, uint32_t* dst
   return j;
 }
 
-// Re-lay two operands' scales into the workspace (one launch).
-int launch_relayout(const ScaleJob& a, const ScaleJob& b, hipStream_t st, const char* what) {
+// Re-lay two operands' scales into the workspace, and, given a pair job,
+// an operand's data into row pairs (one launch).
+int launch_relayout(const ScaleJob& a, const ScaleJob& b, hipStream_t st, const char* what,
+                    const PairJob* d = nullptr) {
   ScaleJobs js;
   js.j[0] = a;
   js.j[1] = b;
   js.tiles0 = a.batches * a.tiles_r * a.tiles_t;
-  const int64_t grid = (int64_t)js.tiles0 + (int64_t)b.batches * b.tiles_r * b.tiles_t;
+  const int64_t t01 = (int64_t)js.tiles0 + (int64_t)b.batches * b.tiles_r * b.tiles_t;
+  if (t01 > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "%s: scale re-layout grid too large", what);
+  js.tiles01 = (int)t01;
+  js.d = d ? *d : PairJob{};
+  const int64_t grid = t01 + (d ? (int64_t)d->batches * d->pairs : 0);
   if (grid <= 0) return MXGG_OK;
   if (grid > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "%s: scale re-layout grid too large", what);
   hipLaunchKernelGGL(scale_relayout_kernel, dim3((unsigned)grid), dim3(256), 0, st, js);
@@ -1884,6 +1923,28 @@ static size_t split_area(int64_t tiles, size_t tile_bytes, int64_t nsteps) {
   if (smax > kMaxSplit) smax = kMaxSplit;
   const double want = (double)tiles * (double)smax * (double)tile_bytes;
   return want < (double)kSplitBytes ? (size_t)want : kSplitBytes;
+}
+
+// Row stride of a weight staged in row pairs (K bytes rounded up to 64).
+static int64_t staged_ld(int64_t K) { return (K + 63) / 64 * 64; }
+
+// Extra workspace for staging an e4m3 weight in row pairs, or 0 where the
+// call would not gain from it.  Staging copies the weight once (2 E N K
+// bytes of HBM traffic in the re-layout launch the call makes anyway); the
+// GEMM then copies whole 128-byte lines of it and runs 4-9% faster at
+// K >= 4096 (measured over the sweep shapes, MI355X; 0-6% at K = 2048).
+// Worth it while the copy stays a small fraction of the GEMM: its time over
+// the GEMM's is about 400 E / M at 5 TB/s and 2 PFLOP/s, so E <= M / 8192.
+// 256 bytes of slack keep the staged lines 256-byte aligned.
+static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
+  if (b_fmt != MXGG_FMT_E4M3 || E <= 0 || N <= 0 || N % 2 || K < 4096 || (int64_t)E * 8192 > M) return 0;
+  if ((int64_t)E * (N / 2) > INT32_MAX || K >= (1 << 22)) return 0;   // launch grid, int offsets
+  return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
+}
+
+extern "C" size_t mxgg_grouped_mm_staging_size(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
+  if (M < 0 || K < 0 || K % 32) return 0;
+  return fwd_staging_bytes(E, M, N, K, b_fmt);
 }
 
 extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
@@ -1982,22 +2043,36 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
                           int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
                           int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
                           int out_dtype, int64_t ldo, int block_m, int block_n, int group_m, int xcd,
-                          void* workspace, size_t ws_bytes, void* stream) {
+                          void* workspace, size_t ws_bytes, void* stream, bool may_stage = true) {
   const size_t need = fwd_scale_bytes(E, M, N, K);
   hipStream_t st = (hipStream_t)stream;
   const int64_t T = cdiv(K, STEP);
   uint32_t* wsd = (uint32_t*)workspace;
+  const size_t part_off = align256(need);
+  size_t room = ws_bytes > part_off ? ws_bytes - part_off : 0;
+  // The weight in row pairs, staged at the end of the workspace when it has
+  // room for that on top of the partial tiles (which keep the room they
+  // would have without it: the same split plan, the same bits).
+  const size_t stage = may_stage ? fwd_staging_bytes(E, M, N, K, b_fmt) : 0;
+  PairJob pj{};
+  const bool staged = T > 0 && stage && room >= stage;
+  if (staged) {
+    room -= stage;
+    const int64_t ldp = staged_ld(K);
+    uint8_t* dst = (uint8_t*)align256((size_t)((uint8_t*)workspace + part_off + room));
+    pj = PairJob{B, ldb_n, ldb_e, dst, (int)ldp, (int)(N / 2), E, (int)K};
+  }
   if (T > 0) {
     if (int rc = launch_relayout(scale_job(A_s, ldas, 0, wsd, M, 1, K / 32, T),
                                  scale_job(B_s, ldbs_n, ldbs_e, wsd + T * M, N, E, K / 32, T), st,
-                                 "grouped_mm"))
+                                 "grouped_mm", staged ? &pj : nullptr))
       return rc;
   }
-  const size_t part_off = align256(need);
-  void* part = ws_bytes > part_off ? (void*)((uint8_t*)workspace + part_off) : nullptr;
-  return launch_grouped_mm(A, lda, (const uint8_t*)wsd, B, b_fmt, ldb_n, ldb_e, (const uint8_t*)(wsd + T * M), offs,
-                           E, M, N, K, out, out_dtype, ldo, block_m, block_n, group_m, xcd, 0, part,
-                           part ? ws_bytes - part_off : 0, st);
+  void* part = room ? (void*)((uint8_t*)workspace + part_off) : nullptr;
+  return launch_grouped_mm(A, lda, (const uint8_t*)wsd, staged ? pj.dst : B, b_fmt, staged ? (int64_t)pj.ld_dst : ldb_n,
+                           staged ? N * pj.ld_dst : ldb_e, (const uint8_t*)(wsd + T * M), offs, E, M, N, K, out,
+                           out_dtype, ldo, block_m, block_n, group_m, xcd, staged ? MXGG_B_PAIRS : 0, part, room,
+                           st);
 }
 
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
@@ -2101,7 +2176,7 @@ extern "C" int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint
   if (int rc = scratch_for_device(&ws)) return rc;
   return run_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K, out,
                         out_dtype, ldo, block_m, block_n, group_m, xcd, ws, (size_t)MXGG_NOALLOC_SCRATCH_BYTES,
-                        stream);
+                        stream, false);   // (no weight staging: the scratch keeps its partial-tile room)
 }
 
 extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,

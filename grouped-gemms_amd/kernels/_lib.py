@@ -57,6 +57,7 @@ SIGNATURES = {
     "mxgg_tile_schedule": (_c_i32, [_c_p, _c_i32, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
                                     _c_p, _c_p]),
     "mxgg_grouped_mm_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
+    "mxgg_grouped_mm_staging_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64, _c_i32]),
     "mxgg_grouped_mm": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
                                  _c_p, _c_i32, _c_i64, _c_i64,
                                  _c_p, _c_i64, _c_i64,

@@ -183,6 +183,8 @@ def triton_mxfp8_grouped_mm(
         return out
     a_s = _u8(_rowmajor(input_act_scales))
     b_s = _u8(_rowmajor(weight_scales))
+    # plus room to stage the weight in row pairs where that pays for its copy
+    ws_bytes += lib.mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_grouped_mm(
         a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),

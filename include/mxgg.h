@@ -221,13 +221,27 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            mxgg_grouped_mm_workspace_size(E, M, N, K) bytes, which adds (after
  *            the scales, 256-byte aligned) room for the fp32 partial tiles of a
  *            last, partial round of tiles cut along K (at most 128 MiB; only for
- *            K >= 4096 and short launches).  With less, no tile is cut.
+ *            K >= 4096 and short launches).  With less, no tile is cut.  With
+ *            mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt) bytes more, an
+ *            e4m3 B is first copied into row pairs at the end of the
+ *            workspace (in the scale re-layout launch), which the GEMM reads
+ *            in whole 128-byte lines; the partial tiles keep the room they
+ *            have without it, and the output bits are the same.
  * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
  * rows need no alignment.  Results do not depend on the workspace size beyond
  * fp32 summation order (a cut tile adds its pieces in a fixed order, so
  * repeated calls give identical bits).
  */
 size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
+/*
+ * Workspace bytes, on top of mxgg_grouped_mm_workspace_size, with which
+ * mxgg_grouped_mm stages an e4m3 B in row pairs (E * N * K rounded up to 64,
+ * plus 256), or 0 where the copy would not pay for itself: it is offered for
+ * K >= 4096 and E <= M / 8192 (the copy then costs about 2-5% of the GEMM's
+ * time and saves 4-9%).  No counterpart in the reference, whose Triton kernel
+ * reads B where it lies.
+ */
+size_t mxgg_grouped_mm_staging_size(int E, int64_t M, int64_t N, int64_t K, int b_fmt);
 int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
                     const uint8_t* B, int b_fmt, int64_t ldb_n, int64_t ldb_e,
                     const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,

@@ -245,6 +245,95 @@ def test_sweep_fwd_pairs(gpu, shape):
 
 
 # ---------------------------------------------------------------------------
+# forward on plain scales: the e4m3 weight staged in row pairs by the call
+# ---------------------------------------------------------------------------
+
+def _staged_call(qa, sa, qw, sw, offs_t, out_dtype, ws_bytes):
+    from kernels import _lib
+    lib = _lib.load()
+    M, K = qa.shape
+    E, N = qw.shape[0], qw.shape[1]
+    a, a_s, b, b_s = _u8(qa), _u8(sa), _u8(qw), _u8(sw)
+    code = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}[out_dtype]
+    out = torch.full((M, N), float("nan"), dtype=out_dtype, device=qa.device)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qa.device)
+    print(f"fwd staged E={E} M={M} N={N} K={K} out={out_dtype} ws={ws_bytes}", flush=True)
+    _lib.check(lib.mxgg_grouped_mm(a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),
+                                   b.data_ptr(), 0, b.stride(1), b.stride(0),
+                                   b_s.data_ptr(), b_s.stride(1), b_s.stride(0),
+                                   offs_t.data_ptr(), E, M, N, K, out.data_ptr(), code, out.stride(0),
+                                   0, 0, 0, 0, ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return out, ws
+
+
+@pytest.mark.parametrize("case", [
+    (1, 8192, 512, 4096, "even", torch.bfloat16),     # smallest staged shape: 32 steps, a lone round split
+    (1, 8192, 384, 4128, "odd", torch.bfloat16),      # K % 64 == 32: the staged rows' zero pad
+    (2, 16384, 640, 8192, "odd", torch.float32),      # two experts, partial column tile, f32 out
+    (1, 12000, 256, 5120, "odd", torch.float16),      # tail rows unrouted, f16 out
+], ids=lambda c: "E{}_M{}_N{}_K{}_{}".format(*c[:5]))
+def test_fwd_staged_weight_bitwise(gpu, case):
+    """mxgg_grouped_mm given mxgg_grouped_mm_staging_size more workspace
+    copies an e4m3 weight into row pairs at the end of the workspace (the
+    documented row-pair byte order, zero pad) and returns the bits of the
+    call without staging and of the step-scale call on row-major data."""
+    import random
+    import kernels
+    from kernels import _lib
+    E, M, N, K, kind, out_dtype = case
+    lib = _lib.load()
+    stage = lib.mxgg_grouped_mm_staging_size(E, M, N, K, _lib.FMT_E4M3)
+    assert stage == E * N * ((K + 63) // 64 * 64) + 256
+    offs = _odd_offs(E, M - 100, E + K) if kind == "odd" else \
+        O.generate_jagged_offs(E, M, 32, rng=random.Random(E * 7 + N))
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    a = _x((M, K), M + K, gpu)
+    w = _x((E, N, K), M + K + 1, gpu, 0.05)
+    sa, qa = kernels.to_mx(a)
+    sw, qw = kernels.to_mx(w)
+    full = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
+    plain, _ = _staged_call(qa, sa, qw, sw, o, out_dtype, full)
+    staged, ws = _staged_call(qa, sa, qw, sw, o, out_dtype, full + stage)
+    rows = int(offs[-1])
+    assert torch.equal(staged[:rows].view(torch.uint8), plain[:rows].view(torch.uint8))
+    ssa, _ = kernels.to_mx(a, scale_layout="steps")
+    ssw, _ = kernels.to_mx(w, scale_layout="steps")
+    steps = kernels.triton_mxfp8_grouped_mm(qa, qw, ssa, ssw, o, out_dtype=out_dtype)
+    assert torch.equal(staged[:rows].view(torch.uint8), steps[:rows].view(torch.uint8))
+    # the staged copy: after the partial-tile room the plain call had, 256-byte aligned
+    T = (K + 127) // 128
+    part_off = (4 * T * (M + E * N) + 255) // 256 * 256
+    room = full + stage - part_off - stage
+    base = ws.data_ptr() + part_off + room
+    dst = (base + 255) // 256 * 256 - ws.data_ptr()
+    ldp = (K + 63) // 64 * 64
+    want = torch.zeros((E, N, ldp), dtype=torch.uint8, device=gpu)
+    want[..., :K] = _u8(qw)
+    want = want.view(E, N // 2, 2, ldp // 64, 64).permute(0, 1, 3, 2, 4).reshape(-1)
+    assert torch.equal(ws[dst:dst + want.numel()], want)
+
+
+def test_fwd_drop_in_stages_the_weight(gpu):
+    """The Python drop-in call on plain scales asks for the staging room
+    (benchmark shape E=1, N=2048, K=8192): same bits as the step-scale call."""
+    import random
+    import kernels
+    E, N, K = 1, 2048, 8192
+    offs = O.generate_jagged_offs(E, M_TOKENS, 32, rng=random.Random(3))
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    a = _x((M_TOKENS, K), 21, gpu)
+    w = _x((E, N, K), 22, gpu, 0.05)
+    sa, qa = kernels.to_mx(a)
+    sw, qw = kernels.to_mx(w)
+    ssa, _ = kernels.to_mx(a, scale_layout="steps")
+    ssw, _ = kernels.to_mx(w, scale_layout="steps")
+    got = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, o)
+    ref = kernels.triton_mxfp8_grouped_mm(qa, qw, ssa, ssw, o)
+    assert torch.equal(got.view(torch.uint8), ref.view(torch.uint8))
+
+
+# ---------------------------------------------------------------------------
 # wgrad
 # ---------------------------------------------------------------------------
 
