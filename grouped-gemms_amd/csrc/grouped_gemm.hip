@@ -1931,13 +1931,15 @@ static int64_t staged_ld(int64_t K) { return (K + 63) / 64 * 64; }
 // Extra workspace for staging an e4m3 weight in row pairs, or 0 where the
 // call would not gain from it.  Staging copies the weight once (2 E N K
 // bytes of HBM traffic in the re-layout launch the call makes anyway); the
-// GEMM then copies whole 128-byte lines of it and runs 4-9% faster at
-// K >= 4096 (measured over the sweep shapes, MI355X; 0-6% at K = 2048).
-// Worth it while the copy stays a small fraction of the GEMM: its time over
-// the GEMM's is about 400 E / M at 5 TB/s and 2 PFLOP/s, so E <= M / 8192.
-// 256 bytes of slack keep the staged lines 256-byte aligned.
+// GEMM then copies whole 128-byte lines of it.  Measured over the sweep
+// shapes (MI355X, M = 16640, whole drop-in calls): E = 1 and 2 gain 2-10%
+// at K >= 5120 and 2-3% at K = 2048 with N >= 5120 (nothing at N = K = 2048);
+// E = 4 gains on some shapes and loses up to 3% on others: the copy's time
+// over the GEMM's is about 400 E / M (5 TB/s against 2 PFLOP/s), so
+// E <= M / 8192.  256 bytes of slack keep the staged lines 256-byte aligned.
 static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
-  if (b_fmt != MXGG_FMT_E4M3 || E <= 0 || N <= 0 || N % 2 || K < 4096 || (int64_t)E * 8192 > M) return 0;
+  if (b_fmt != MXGG_FMT_E4M3 || E <= 0 || N <= 0 || N % 2 || (int64_t)E * 8192 > M) return 0;
+  if (K < 2048 || (K < 4096 && N < 4096)) return 0;
   if ((int64_t)E * (N / 2) > INT32_MAX || K >= (1 << 22)) return 0;   // launch grid, int offsets
   return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
 }

@@ -237,9 +237,9 @@ size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
  * Workspace bytes, on top of mxgg_grouped_mm_workspace_size, with which
  * mxgg_grouped_mm stages an e4m3 B in row pairs (E * N * K rounded up to 64,
  * plus 256), or 0 where the copy would not pay for itself: it is offered for
- * K >= 4096 and E <= M / 8192 (the copy then costs about 2-5% of the GEMM's
- * time and saves 4-9%).  No counterpart in the reference, whose Triton kernel
- * reads B where it lies.
+ * E <= M / 8192 and K >= 4096, or K >= 2048 with N >= 4096 (the copy then
+ * costs about 2-5% of the GEMM's time and saves more).  No counterpart in the
+ * reference, whose Triton kernel reads B where it lies.
  */
 size_t mxgg_grouped_mm_staging_size(int E, int64_t M, int64_t N, int64_t K, int b_fmt);
 int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,

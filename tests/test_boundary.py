@@ -120,13 +120,16 @@ def test_grouped_mm_workspace_without_gpu():
     # wgrad E=1, M=2048: 16 steps -> no split
     assert lib.mxgg_wgrad_workspace_size(1, 2048, 256, 256) == 4 * 16 * (256 + 256)
     # staging an e4m3 weight in row pairs: E * N * K rounded up to 64, plus 256
-    # bytes of alignment slack, offered for K >= 4096 and E <= M / 8192 only
+    # bytes of alignment slack, offered for E <= M / 8192 and K >= 4096 (or
+    # K >= 2048 with N >= 4096) only
     E4M3, E2M1 = _lib.FMT_E4M3, _lib.FMT_E2M1
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 2048, 8192, E4M3) == 2048 * 8192 + 256
     assert lib.mxgg_grouped_mm_staging_size(2, 16640, 5120, 4128, E4M3) == 2 * 5120 * 4160 + 256
     assert lib.mxgg_grouped_mm_staging_size(2, 16384, 5120, 5120, E4M3) == 2 * 5120 * 5120 + 256
     assert lib.mxgg_grouped_mm_staging_size(3, 16384, 5120, 5120, E4M3) == 0     # E > M / 8192
-    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 2048, E4M3) == 0     # K < 4096
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 2048, 2048, E4M3) == 0     # K, N < 4096
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 2048, E4M3) == 8192 * 2048 + 256
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 1024, E4M3) == 0     # K < 2048
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8191, 8192, E4M3) == 0     # odd N: no row pairs
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8192, E2M1) == 0     # e4m3 weights only
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8200, E4M3) == 0     # K % 32
