@@ -107,6 +107,8 @@ def triton_mxfp8_wgrad(
         return out
     gs = _u8(_rowmajor(go_scale))
     as_ = _u8(_rowmajor(ia_scale))
+    # plus room to stage both operands in row pairs where that pays for its copy
+    ws_bytes += lib.mxgg_wgrad_staging_size(E, M, N, K)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_wgrad(
         g.data_ptr(), g.stride(0), gs.data_ptr(), gs.stride(0),

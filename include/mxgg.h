@@ -311,9 +311,21 @@ int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
  *         for the fp32 partial tiles of tiles cut along the token range when
  *         the tiles do not fill the chip (E = 1, or fewer tiles than
  *         resident workgroups; with E > 1 sized for a group of all M tokens,
- *         since the kernels cut by the longest group), at most 128 MiB.
+ *         since the kernels cut by the longest group), at most 128 MiB.  With
+ *         mxgg_wgrad_staging_size(E, M, N, K) bytes more, go_t and ia_t are
+ *         first copied into row pairs at the end of the workspace (in the
+ *         scale re-layout launch) and the GEMM reads whole 128-byte lines of
+ *         them; the partial tiles keep their room, the output bits are the same.
  */
 size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
+/*
+ * Workspace bytes, on top of mxgg_wgrad_workspace_size, with which mxgg_wgrad
+ * stages both operands in row pairs ((N + K) * M rounded up to 64, plus 512),
+ * or 0 where the copy would not pay for itself: it is left out for N + K <
+ * 10240 with E * (N + K) <= 8192 (small reductions in few groups), for odd N
+ * or K, and for M not a multiple of 32.  No counterpart in the reference.
+ */
+size_t mxgg_wgrad_staging_size(int E, int64_t M, int64_t N, int64_t K);
 int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
                const uint8_t* ia_t, int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias,
                const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,

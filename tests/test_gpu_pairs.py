@@ -371,6 +371,71 @@ def test_wgrad_pairs_bitwise(gpu, case):
     _wgrad_all_layouts(gpu, E, M, N, K, offs, seed=N + K)
 
 
+def _wgrad_plain_call(qg, sg, qi, si, offs_t, out_dtype, ws_bytes):
+    from kernels import _lib
+    lib = _lib.load()
+    N, M = qg.shape
+    K = qi.shape[0]
+    E = offs_t.numel()
+    g, gs, i, is_ = _u8(qg), _u8(sg), _u8(qi), _u8(si)
+    code = {torch.bfloat16: 0, torch.float32: 2}[out_dtype]
+    out = torch.full((E, N, K), float("nan"), dtype=out_dtype, device=qg.device)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qg.device)
+    print(f"wgrad staged E={E} M={M} N={N} K={K} out={out_dtype} ws={ws_bytes}", flush=True)
+    _lib.check(lib.mxgg_wgrad(g.data_ptr(), g.stride(0), gs.data_ptr(), gs.stride(0), i.data_ptr(), i.stride(0),
+                              is_.data_ptr(), is_.stride(0), offs_t.data_ptr(), E, M, N, K, out.data_ptr(), code,
+                              ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return out, ws
+
+
+def _pairs_bytes(q, rows, L, dev):
+    """Row-pair bytes of a row-major (rows, L) e4m3 operand, per the header's formula."""
+    ldp = (L + 63) // 64 * 64
+    want = torch.zeros((rows, ldp), dtype=torch.uint8, device=dev)
+    want[:, :L] = _u8(q)
+    return want.view(rows // 2, 2, ldp // 64, 64).permute(0, 2, 1, 3).reshape(-1)
+
+
+@pytest.mark.parametrize("case", [
+    (8, 4096, 768, 640, "odd", torch.bfloat16),        # many small groups, bounds off the 16 grid
+    (2, 2080, 2048, 5120, "even", torch.bfloat16),     # 2080 tokens: rows padded to 2112 when staged
+    (1, 8192, 5120, 5120, "even", torch.float32),      # E = 1, tiles cut along the tokens, f32 out
+], ids=lambda c: "E{}_M{}_N{}_K{}_{}".format(*c[:5]))
+def test_wgrad_staged_operands_bitwise(gpu, case):
+    """mxgg_wgrad given mxgg_wgrad_staging_size more workspace copies go_t
+    and ia_t into row pairs at the end of the workspace (the documented byte
+    order, zero pad) and returns the bits of the call without staging and of
+    the step-scale call on row-major data."""
+    import random
+    import kernels
+    from kernels import _lib
+    E, M, N, K, kind, out_dtype = case
+    lib = _lib.load()
+    ldp = (M + 63) // 64 * 64
+    stage = lib.mxgg_wgrad_staging_size(E, M, N, K)
+    assert stage == (N + K) * ldp + 512
+    offs = _odd_offs(E, M, E + N) if kind == "odd" else O.generate_jagged_offs(E, M, 32, rng=random.Random(E + M))
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    go = _x((M, N), N + K, gpu, 0.5)
+    ia = _x((M, K), N + K + 1, gpu)
+    sg, qg = kernels.to_mx_dim0(go)
+    si, qi = kernels.to_mx_dim0(ia)
+    full = lib.mxgg_wgrad_workspace_size(E, M, N, K)
+    plain, _ = _wgrad_plain_call(qg, sg, qi, si, o, out_dtype, full)
+    staged, ws = _wgrad_plain_call(qg, sg, qi, si, o, out_dtype, full + stage)
+    assert torch.equal(staged.view(torch.uint8), plain.view(torch.uint8))
+    ssg, _ = kernels.to_mx_dim0(go, scale_layout="steps")
+    ssi, _ = kernels.to_mx_dim0(ia, scale_layout="steps")
+    steps = kernels.triton_mxfp8_wgrad(qg, ssg, qi, ssi, o, out_dtype=out_dtype)
+    assert torch.equal(staged.view(torch.uint8), steps.view(torch.uint8))
+    base = ws.data_ptr() + full          # where the partial-tile room of the unstaged call ends
+    dg = (base + 255) // 256 * 256 - ws.data_ptr()
+    di = (ws.data_ptr() + dg + N * ldp + 255) // 256 * 256 - ws.data_ptr()
+    assert torch.equal(ws[dg:dg + N * ldp], _pairs_bytes(qg, N, M, gpu))
+    assert torch.equal(ws[di:di + K * ldp], _pairs_bytes(qi, K, M, gpu))
+
+
 def test_wgrad_pairs_from_the_quantizer_f32(gpu):
     _wgrad_all_layouts(gpu, 5, 2080, 384, 256, _odd_offs(5, 2080, 1), seed=3, out_dtype=torch.float32,
                        quantizer_pairs=True)
