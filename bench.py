@@ -151,7 +151,8 @@ def copy_calibration(dev, mib: int = 256, reps: int = 3):
     del src, dst
 
 
-def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shapes: int) -> str:
+def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shapes: int,
+                kernel_only: bool = False) -> str:
     """HBM bytes per launch of each GEMM kernel from two rocprofv3 --pmc passes
     (FETCH_SIZE, WRITE_SIZE; KiB per dispatch) over
     ``bench.py --steps S --warmup W --no-cpu --no-bf16 --no-extra --copy-calibration``.
@@ -184,11 +185,12 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
         scaled[counter] = [(n, v * factor * 1024.0) for _, n, v in rows
                            if ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n]
     f, w = scaled["FETCH_SIZE"], scaled["WRITE_SIZE"]
-    # each call is timed twice (plain scales, then step-major), warmup + steps
-    # launches each; the native sweep times each call once
+    # each call is timed twice (plain scales, then step-major; with
+    # --kernel-only step-major only), warmup + steps launches each; the
+    # native sweep times each call once
     shapes = SHAPES[:n_shapes]
     want = []
-    for tag, per in (("", 2 * (warmup + steps)), (NATIVE_TAG, warmup + steps)):
+    for tag, per in (("", (1 if kernel_only else 2) * (warmup + steps)), (NATIVE_TAG, warmup + steps)):
         for (e, n, k) in shapes:
             for kind in ("fwd", "dgrad", "wgrad"):
                 if kind == "wgrad":
@@ -662,14 +664,18 @@ def main():
                     help="skip the second sweep on row-pair data (the native layout)")
     ap.add_argument("--native-only", action="store_true",
                     help="run only the sweep on row-pair data (for counter passes of that layout)")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="time only the calls on step-major scales (the row-major kernel-only figures), not the "
+                         "drop-in calls, which may stage operands in row pairs: for counter passes of the "
+                         "row-major layout")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the BASELINE config 5 (e4m3 x e2m1) and quantizer measurements")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 plain 256 MiB device copies (PMC byte-counter calibration)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarize two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of "
-                         "`bench.py --steps S --warmup W --no-cpu --copy-calibration` (same S, W, --shapes) "
-                         "and exit; runs on the CPU")
+                         "`bench.py --steps S --warmup W --no-cpu --copy-calibration [--kernel-only]` (same S, W, "
+                         "--shapes, --kernel-only) and exit; runs on the CPU")
     ap.add_argument("--counter-summary", metavar="COUNTER_CSV",
                     help="per-kernel means of a rocprofv3 --pmc counter CSV and exit; runs on the CPU")
     ap.add_argument("--stats-summary", nargs="+", metavar="CSV",
@@ -684,7 +690,8 @@ def main():
         print(stats_summary(*args.stats_summary))
         return
     if args.pmc_summary:
-        print(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.steps, args.warmup, args.shapes))
+        print(pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.steps, args.warmup, args.shapes,
+                          args.kernel_only))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -754,12 +761,13 @@ def main():
                 row["bf16_tflops"] = flops / (bmed * 1e-3) / 1e12
                 del wk
             del a, w
-            med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs),
-                                  args.steps, args.warmup, flush)
-            row["fwd_us"] = med * 1e3
-            row["fwd_tflops"] = flops / (med * 1e-3) / 1e12
-            if "bf16_us" in row:
-                row["fwd_speedup_vs_bf16"] = row["bf16_us"] / row["fwd_us"]
+            if not args.kernel_only:
+                med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs),
+                                      args.steps, args.warmup, flush)
+                row["fwd_us"] = med * 1e3
+                row["fwd_tflops"] = flops / (med * 1e-3) / 1e12
+                if "bf16_us" in row:
+                    row["fwd_speedup_vs_bf16"] = row["bf16_us"] / row["fwd_us"]
             kernel_only("fwd_kernel_us", lambda: triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs),
                         fwd_kernel_name(_pick_config(E, M, N, K)), flops, row)
             del qa, qw, sa, sw, ta, tw
@@ -771,10 +779,11 @@ def main():
             tg, _ = to_mx(go, scale_layout="steps")
             tt, _ = to_mx(wt, scale_layout="steps")
             del go, wt
-            med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qg, qt, sg, st_, offs),
-                                  args.steps, args.warmup, flush)
-            row["dgrad_us"] = med * 1e3
-            row["dgrad_tflops"] = flops / (med * 1e-3) / 1e12
+            if not args.kernel_only:
+                med, mean = time_call(lambda: triton_mxfp8_grouped_mm(qg, qt, sg, st_, offs),
+                                      args.steps, args.warmup, flush)
+                row["dgrad_us"] = med * 1e3
+                row["dgrad_tflops"] = flops / (med * 1e-3) / 1e12
             kernel_only("dgrad_kernel_us", lambda: triton_mxfp8_grouped_mm(qg, qt, tg, tt, offs),
                         fwd_kernel_name(_pick_config(E, M, K, N)), flops, row)
             del qg, qt, sg, st_, tg, tt
@@ -786,10 +795,11 @@ def main():
             tg, _ = to_mx_dim0(go, scale_layout="steps")
             ti, _ = to_mx_dim0(ia, scale_layout="steps")
             del go, ia
-            med, mean = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs),
-                                  args.steps, args.warmup, flush)
-            row["wgrad_us"] = med * 1e3
-            row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
+            if not args.kernel_only:
+                med, mean = time_call(lambda: triton_mxfp8_wgrad(qg, sg, qi, si, offs),
+                                      args.steps, args.warmup, flush)
+                row["wgrad_us"] = med * 1e3
+                row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
             kernel_only("wgrad_kernel_us", lambda: triton_mxfp8_wgrad(qg, tg, qi, ti, offs), WGRAD_KERNEL, flops, row)
             del qg, qi, sg, si, tg, ti
         torch.cuda.empty_cache()
@@ -828,8 +838,9 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
     value = fwd_gm if fwd_gm is not None else (dgrad_gm or wgrad_gm)
-    if value is None:            # --native-only: nothing row-major was timed
-        value = next((v for v in kernel_geomeans(rows, "_native_us").values() if v), 0.0)
+    if value is None:            # --kernel-only / --native-only: no drop-in call was timed
+        value = next((v for v in list(kernel_geomeans(rows, "_kernel_us").values()) +
+                      list(kernel_geomeans(rows, "_native_us").values()) if v), 0.0)
     line = {
         "metric": "geomean MXFP8 grouped-GEMM TFLOPs (% of MXFP8 peak), fwd/dgrad/wgrad, 1 GPU",
         "value": round(value, 1),
