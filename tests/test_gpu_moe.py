@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import f32, randn_bf16, seeded_offs
+from helpers import bits_u8, bits_u16, f32, randn_bf16, seeded_offs
 from oracle import mx_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -51,6 +51,12 @@ def test_to_mx_both_matches_separate_quantizers(gpu, dtype, shape):
         hq = (q_c if x.dim() == 3 else q_c.unsqueeze(0))[b]
         assert torch.equal(gr, rs) and torch.equal(gq.view(torch.uint8), rq.view(torch.uint8))
         assert torch.equal(hc, cs) and torch.equal(hq.view(torch.uint8), cq.view(torch.uint8))
+        # and directly against the oracle's to_mx, specials included, both layouts
+        for t, sc, qq in ((xs[b].cpu(), gr, gq), (xs[b].cpu().t().contiguous(), hc, hq)):
+            src = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[t.dtype]
+            ref_s, ref_q = O.to_mx(bits_u16(t), src=src) if src == "bf16" else O.to_mx(t.numpy(), src=src)
+            np.testing.assert_array_equal(bits_u8(sc), ref_s)
+            np.testing.assert_array_equal(bits_u8(qq), ref_q)
 
 
 def _sqnr(ref, x):
