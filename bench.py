@@ -869,6 +869,10 @@ def main():
         "fwd_speedup_vs_bf16_geomean": round(speedup_gm, 3) if speedup_gm else None,
         "fwd_speedup_vs_readme_bf16": round(fwd_gm / REF_BF16_GEOMEAN_TFLOPS, 3) if fwd_gm else None,
         "ref_speedup_vs_bf16_geomean": REF_SPEEDUP_VS_BF16,
+        "drop_in_staging": "inside the timed drop-in calls, the re-layout launch also copies an e4m3 weight "
+                           "(forward / dgrad, E <= M/8192, K >= 4096 or N >= 4096) or both wgrad operands (unless "
+                           "N + K < 10240 and E*(N+K) <= 8192) into row pairs, which the GEMM reads in whole "
+                           "128-byte lines; same bits as without (mxgg_*_staging_size)",
         "kernel_only_geomean_tflops": kernel_geomeans(rows, "_kernel_us"),
         "native_geomean_tflops": kernel_geomeans(rows, "_native_us"),
         "native_layout": "kernel-only time on the layout the kernels read fastest: step-major scales and row-pair "
