@@ -2072,7 +2072,7 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
                           int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
                           int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
                           int out_dtype, int64_t ldo, int block_m, int block_n, int group_m, int xcd,
-                          void* workspace, size_t ws_bytes, void* stream, bool may_stage = true) {
+                          void* workspace, size_t ws_bytes, void* stream) {
   const size_t need = fwd_scale_bytes(E, M, N, K);
   hipStream_t st = (hipStream_t)stream;
   const int64_t T = cdiv(K, STEP);
@@ -2082,7 +2082,7 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
   // The weight in row pairs, staged at the end of the workspace when it has
   // room for that on top of the partial tiles (which keep the room they
   // would have without it: the same split plan, the same bits).
-  const size_t stage = may_stage ? fwd_staging_bytes(E, M, N, K, b_fmt) : 0;
+  const size_t stage = fwd_staging_bytes(E, M, N, K, b_fmt);
   PairJob pj{};
   const bool staged = T > 0 && stage && room >= stage;
   if (staged) {
@@ -2151,10 +2151,12 @@ extern "C" int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32
 
 // MXGG_NOALLOC_SCRATCH_BYTES per device, held from the library's load to the
 // end of the process: the re-laid scales of a call (4 * cdiv(K, 128) *
-// (M + E*N) bytes; 21 MB for the largest sweep shape) and, after them, the
-// fp32 partial tiles of a split last round.  Nothing in it needs clearing:
-// every call writes the scales before reading them, and a split call writes
-// every partial tile before the reduce reads it.
+// (M + E*N) bytes; 21 MB for the largest sweep shape), after them the fp32
+// partial tiles of a split last round, and, at the end, a weight staged in
+// row pairs when that fits as well (as for a caller's workspace of this
+// size).  Nothing in it needs clearing: every call writes the scales and the
+// staged weight before reading them, and a split call writes every partial
+// tile before the reduce reads it.
 static __device__ __align__(256) uint8_t scratch[MXGG_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -2205,7 +2207,7 @@ extern "C" int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint
   if (int rc = scratch_for_device(&ws)) return rc;
   return run_grouped_mm(A, lda, A_s, ldas, B, b_fmt, ldb_n, ldb_e, B_s, ldbs_n, ldbs_e, offs, E, M, N, K, out,
                         out_dtype, ldo, block_m, block_n, group_m, xcd, ws, (size_t)MXGG_NOALLOC_SCRATCH_BYTES,
-                        stream, false);   // (no weight staging: the scratch keeps its partial-tile room)
+                        stream);
 }
 
 extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,

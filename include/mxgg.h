@@ -276,7 +276,8 @@ int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32_t* A_ss,
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid allocation).  Same arguments,
  * results and errors as mxgg_grouped_mm given a workspace of
- * MXGG_NOALLOC_SCRATCH_BYTES bytes; the workspace is instead a device array
+ * MXGG_NOALLOC_SCRATCH_BYTES bytes (the weight staging included, where it
+ * fits); the workspace is instead a device array
  * inside this library, one per GPU, allocated when the library is loaded and
  * held until the process ends.  Calls it cannot take -- the re-laid scales,
  * 4 * ceil(K/128) * (M + E*N) bytes, above MXGG_NOALLOC_SCRATCH_BYTES -- are

@@ -41,7 +41,8 @@ def test_noalloc_matches_workspace_entry_point(gpu):
     ws = torch.empty(_lib.NOALLOC_SCRATCH_BYTES, dtype=torch.uint8, device=gpu)
     # first call: a sweep shape whose last round is split (partial tiles in the
     # array after the scales); second: smaller, with ragged and empty groups
-    for E, M, N, K, offs in ((8, 16640, 2048, 5120, seeded_offs(8, 16640, seed=5)),
+    for E, M, N, K, offs in ((1, 16640, 2048, 8192, np.array([16000], np.int32)),       # weight staged too
+                             (8, 16640, 2048, 5120, seeded_offs(8, 16640, seed=5)),
                              (4, 1000, 384, 256, np.array([0, 300, 300, 992], np.int32))):
         print(f"noalloc E={E} M={M} N={N} K={K} offs={list(offs)}", flush=True)
         qa, sa, qb, sb = _operands(E, M, N, K, seed=E + K, dev=gpu)
