@@ -870,7 +870,8 @@ def main():
         "fwd_speedup_vs_readme_bf16": round(fwd_gm / REF_BF16_GEOMEAN_TFLOPS, 3) if fwd_gm else None,
         "ref_speedup_vs_bf16_geomean": REF_SPEEDUP_VS_BF16,
         "drop_in_staging": "inside the timed drop-in calls, the re-layout launch also copies an e4m3 weight "
-                           "(forward / dgrad, E <= M/8192, K >= 4096 or N >= 4096) or both wgrad operands (unless "
+                           "(forward / dgrad, E <= M/8192, K >= 4096 or N >= 4096), A (N >= 8192), or both wgrad "
+                           "operands (unless "
                            "N + K < 10240 and E*(N+K) <= 8192) into row pairs, which the GEMM reads in whole "
                            "128-byte lines; same bits as without (mxgg_*_staging_size)",
         "kernel_only_geomean_tflops": kernel_geomeans(rows, "_kernel_us"),

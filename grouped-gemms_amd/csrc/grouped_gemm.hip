@@ -1952,6 +1952,17 @@ static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fm
   return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
 }
 
+// The same for A (M, K), or 0: its copy's time over the GEMM's is about
+// 400 / N, and staging it paid at N >= 8192 on every sweep shape (drop-in
+// call, same box: -1 to -12% at E = 4 and 8, where the weight is not staged;
+// -0.1 to -6% at E = 1 and 2 on top of the staged weight), not reliably at
+// N = 5120 (-6% to +1.4%).
+static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
+  if (b_fmt != MXGG_FMT_E4M3 || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
+  if (M / 2 > INT32_MAX || K >= (1 << 22)) return 0;
+  return (size_t)M * (size_t)staged_ld(K) + 256;
+}
+
 // Extra workspace for staging both wgrad operands (go_t (N, M), ia_t (K, M))
 // in row pairs, or 0 where that would not pay.  The copy moves 2 (N + K) M
 // bytes in the scale re-layout launch; the GEMM then copies whole lines
@@ -1972,8 +1983,8 @@ extern "C" size_t mxgg_wgrad_staging_size(int E, int64_t M, int64_t N, int64_t K
 }
 
 extern "C" size_t mxgg_grouped_mm_staging_size(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
-  if (M < 0 || K < 0 || K % 32) return 0;
-  return fwd_staging_bytes(E, M, N, K, b_fmt);
+  if (M < 0 || K < 0 || K % 32 || E <= 0) return 0;
+  return fwd_staging_bytes(E, M, N, K, b_fmt) + fwd_staging_bytes_a(M, N, K, b_fmt);
 }
 
 extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
@@ -2079,29 +2090,37 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
   uint32_t* wsd = (uint32_t*)workspace;
   const size_t part_off = align256(need);
   size_t room = ws_bytes > part_off ? ws_bytes - part_off : 0;
-  // The weight in row pairs, staged at the end of the workspace when it has
-  // room for that on top of the partial tiles (which keep the room they
-  // would have without it: the same split plan, the same bits).
-  const size_t stage = fwd_staging_bytes(E, M, N, K, b_fmt);
-  PairJob pj{};
-  const bool staged = T > 0 && stage && room >= stage;
-  if (staged) {
-    room -= stage;
-    const int64_t ldp = staged_ld(K);
+  // The weight, then A, in row pairs, staged at the end of the workspace
+  // (the weight last) when it has room for them on top of the partial tiles
+  // (which keep the room they would have without them: the same split plan,
+  // the same bits).
+  const size_t stage_b = fwd_staging_bytes(E, M, N, K, b_fmt), stage_a = fwd_staging_bytes_a(M, N, K, b_fmt);
+  const int ldp = (int)staged_ld(K);
+  PairJob pb{}, pa{};
+  const bool staged_b = T > 0 && stage_b && room >= stage_b;
+  if (staged_b) {
+    room -= stage_b;
     uint8_t* dst = (uint8_t*)align256((size_t)((uint8_t*)workspace + part_off + room));
-    pj = PairJob{B, ldb_n, ldb_e, dst, (int)ldp, (int)(N / 2), E, (int)K};
+    pb = PairJob{B, ldb_n, ldb_e, dst, ldp, (int)(N / 2), E, (int)K};
+  }
+  const bool staged_a = T > 0 && stage_a && room >= stage_a;
+  if (staged_a) {
+    room -= stage_a;
+    uint8_t* dst = (uint8_t*)align256((size_t)((uint8_t*)workspace + part_off + room));
+    pa = PairJob{A, lda, 0, dst, ldp, (int)(M / 2), 1, (int)K};
   }
   if (T > 0) {
     if (int rc = launch_relayout(scale_job(A_s, ldas, 0, wsd, M, 1, K / 32, T),
-                                 scale_job(B_s, ldbs_n, ldbs_e, wsd + T * M, N, E, K / 32, T), st,
-                                 "grouped_mm", staged ? &pj : nullptr))
+                                 scale_job(B_s, ldbs_n, ldbs_e, wsd + T * M, N, E, K / 32, T), st, "grouped_mm",
+                                 staged_b ? &pb : nullptr, staged_a ? &pa : nullptr))
       return rc;
   }
   void* part = room ? (void*)((uint8_t*)workspace + part_off) : nullptr;
-  return launch_grouped_mm(A, lda, (const uint8_t*)wsd, staged ? pj.dst : B, b_fmt, staged ? (int64_t)pj.ld_dst : ldb_n,
-                           staged ? N * pj.ld_dst : ldb_e, (const uint8_t*)(wsd + T * M), offs, E, M, N, K, out,
-                           out_dtype, ldo, block_m, block_n, group_m, xcd, staged ? MXGG_B_PAIRS : 0, part, room,
-                           st);
+  return launch_grouped_mm(staged_a ? pa.dst : A, staged_a ? (int64_t)ldp : lda, (const uint8_t*)wsd,
+                           staged_b ? pb.dst : B, b_fmt, staged_b ? (int64_t)ldp : ldb_n,
+                           staged_b ? N * ldp : ldb_e, (const uint8_t*)(wsd + T * M), offs, E, M, N, K, out,
+                           out_dtype, ldo, block_m, block_n, group_m, xcd,
+                           (staged_b ? MXGG_B_PAIRS : 0) | (staged_a ? MXGG_A_PAIRS : 0), part, room, st);
 }
 
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,

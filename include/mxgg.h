@@ -223,10 +223,10 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            last, partial round of tiles cut along K (at most 128 MiB; only for
  *            K >= 4096 and short launches).  With less, no tile is cut.  With
  *            mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt) bytes more, an
- *            e4m3 B is first copied into row pairs at the end of the
- *            workspace (in the scale re-layout launch), which the GEMM reads
- *            in whole 128-byte lines; the partial tiles keep the room they
- *            have without it, and the output bits are the same.
+ *            e4m3 B and / or A is first copied into row pairs at the end of
+ *            the workspace (in the scale re-layout launch), which the GEMM
+ *            reads in whole 128-byte lines; the partial tiles keep the room
+ *            they have without it, and the output bits are the same.
  * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
  * rows need no alignment.  Results do not depend on the workspace size beyond
  * fp32 summation order (a cut tile adds its pieces in a fixed order, so
@@ -235,11 +235,12 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
 size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 /*
  * Workspace bytes, on top of mxgg_grouped_mm_workspace_size, with which
- * mxgg_grouped_mm stages an e4m3 B in row pairs (E * N * K rounded up to 64,
- * plus 256), or 0 where the copy would not pay for itself: it is offered for
- * E <= M / 8192 and K >= 4096, or K >= 2048 with N >= 4096 (the copy then
- * costs about 2-5% of the GEMM's time and saves more).  No counterpart in the
- * reference, whose Triton kernel reads B where it lies.
+ * mxgg_grouped_mm stages e4m3 operands in row pairs, or 0 where the copies
+ * would not pay for themselves: B (E * N * K rounded up to 64, plus 256) for
+ * E <= M / 8192 and K >= 4096, or K >= 2048 with N >= 4096; A (M * K rounded
+ * up to 64, plus 256) for N >= 8192, K >= 2048 and M even.  The copies then
+ * cost a few percent of the GEMM's time and save more.  No counterpart in the
+ * reference, whose Triton kernel reads its operands where they lie.
  */
 size_t mxgg_grouped_mm_staging_size(int E, int64_t M, int64_t N, int64_t K, int b_fmt);
 int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,

@@ -128,10 +128,13 @@ def test_grouped_mm_workspace_without_gpu():
     assert lib.mxgg_grouped_mm_staging_size(2, 16384, 5120, 5120, E4M3) == 2 * 5120 * 5120 + 256
     assert lib.mxgg_grouped_mm_staging_size(3, 16384, 5120, 5120, E4M3) == 0     # E > M / 8192
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 2048, 2048, E4M3) == 0     # K, N < 4096
-    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 2048, E4M3) == 8192 * 2048 + 256
+    # ... plus A (M * K rounded up to 64, plus 256) for N >= 8192, K >= 2048, M even
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 2048, E4M3) == 8192 * 2048 + 256 + 16640 * 2048 + 256
+    assert lib.mxgg_grouped_mm_staging_size(8, 16640, 8192, 5120, E4M3) == 16640 * 5120 + 256   # A only
+    assert lib.mxgg_grouped_mm_staging_size(8, 16641, 8192, 5120, E4M3) == 0                  # odd M
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 1024, E4M3) == 0     # K < 2048
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8191, 8192, E4M3) == 0     # odd N: no row pairs
-    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8192, E2M1) == 0     # e4m3 weights only
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8192, E2M1) == 0     # e4m3 operands only
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8200, E4M3) == 0     # K % 32
     # wgrad: both operands, (N + K) * M rounded up to 64, plus 512; not for N + K < 10240 with
     # E * (N + K) <= 8192, odd N or K, or M off the 32 grid

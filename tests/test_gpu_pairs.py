@@ -272,19 +272,25 @@ def _staged_call(qa, sa, qw, sw, offs_t, out_dtype, ws_bytes):
     (1, 8192, 384, 4128, "odd", torch.bfloat16),      # K % 64 == 32: the staged rows' zero pad
     (2, 16384, 640, 8192, "odd", torch.float32),      # two experts, partial column tile, f32 out
     (1, 12000, 256, 5120, "odd", torch.float16),      # tail rows unrouted, f16 out
+    (1, 8192, 8192, 2048, "odd", torch.bfloat16),     # N = 8192: A staged as well
+    (4, 8192, 8192, 2080, "odd", torch.bfloat16),     # A staged alone (E > M / 8192), K % 64 == 32
 ], ids=lambda c: "E{}_M{}_N{}_K{}_{}".format(*c[:5]))
 def test_fwd_staged_weight_bitwise(gpu, case):
     """mxgg_grouped_mm given mxgg_grouped_mm_staging_size more workspace
-    copies an e4m3 weight into row pairs at the end of the workspace (the
-    documented row-pair byte order, zero pad) and returns the bits of the
-    call without staging and of the step-scale call on row-major data."""
+    copies an e4m3 weight (and, at N >= 8192, A) into row pairs at the end of
+    the workspace (the documented row-pair byte order, zero pad) and returns
+    the bits of the call without staging and of the step-scale call on
+    row-major data."""
     import random
     import kernels
     from kernels import _lib
     E, M, N, K, kind, out_dtype = case
     lib = _lib.load()
     stage = lib.mxgg_grouped_mm_staging_size(E, M, N, K, _lib.FMT_E4M3)
-    assert stage == E * N * ((K + 63) // 64 * 64) + 256
+    ldp = (K + 63) // 64 * 64
+    stage_b = E * N * ldp + 256 if E * 8192 <= M and (K >= 4096 or (K >= 2048 and N >= 4096)) else 0
+    stage_a = M * ldp + 256 if N >= 8192 and K >= 2048 and M % 2 == 0 else 0
+    assert stage == stage_b + stage_a > 0
     offs = _odd_offs(E, M - 100, E + K) if kind == "odd" else \
         O.generate_jagged_offs(E, M, 32, rng=random.Random(E * 7 + N))
     o = torch.tensor(offs, dtype=torch.int32, device=gpu)
@@ -301,17 +307,21 @@ def test_fwd_staged_weight_bitwise(gpu, case):
     ssw, _ = kernels.to_mx(w, scale_layout="steps")
     steps = kernels.triton_mxfp8_grouped_mm(qa, qw, ssa, ssw, o, out_dtype=out_dtype)
     assert torch.equal(staged[:rows].view(torch.uint8), steps[:rows].view(torch.uint8))
-    # the staged copy: after the partial-tile room the plain call had, 256-byte aligned
-    T = (K + 127) // 128
-    part_off = (4 * T * (M + E * N) + 255) // 256 * 256
-    room = full + stage - part_off - stage
-    base = ws.data_ptr() + part_off + room
-    dst = (base + 255) // 256 * 256 - ws.data_ptr()
-    ldp = (K + 63) // 64 * 64
-    want = torch.zeros((E, N, ldp), dtype=torch.uint8, device=gpu)
-    want[..., :K] = _u8(qw)
-    want = want.view(E, N // 2, 2, ldp // 64, 64).permute(0, 1, 3, 2, 4).reshape(-1)
-    assert torch.equal(ws[dst:dst + want.numel()], want)
+    # the staged copies after the partial-tile room the plain call had, each
+    # 256-byte aligned: the weight at the end, A before it
+    end = ws.data_ptr() + full + stage
+    if stage_b:
+        dst = (end - stage_b + 255) // 256 * 256 - ws.data_ptr()
+        want = torch.zeros((E, N, ldp), dtype=torch.uint8, device=gpu)
+        want[..., :K] = _u8(qw)
+        want = want.view(E, N // 2, 2, ldp // 64, 64).permute(0, 1, 3, 2, 4).reshape(-1)
+        assert torch.equal(ws[dst:dst + want.numel()], want)
+    if stage_a:
+        dst = (end - stage_b - stage_a + 255) // 256 * 256 - ws.data_ptr()
+        want = torch.zeros((M, ldp), dtype=torch.uint8, device=gpu)
+        want[:, :K] = _u8(qa)
+        want = want.view(M // 2, 2, ldp // 64, 64).permute(0, 2, 1, 3).reshape(-1)
+        assert torch.equal(ws[dst:dst + want.numel()], want)
 
 
 def test_fwd_drop_in_stages_the_weight(gpu):
