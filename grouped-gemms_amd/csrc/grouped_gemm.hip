@@ -1955,10 +1955,11 @@ static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fm
 // The same for A (M, K), or 0: its copy's time over the GEMM's is about
 // 400 / N, and staging it paid at N >= 8192 on every sweep shape (drop-in
 // call, same box: -1 to -12% at E = 4 and 8, where the weight is not staged;
-// -0.1 to -6% at E = 1 and 2 on top of the staged weight), not reliably at
-// N = 5120 (-6% to +1.4%).
+// -0.1 to -6% at E = 1 and 2 on top of the staged weight; with e2m1
+// weights, BASELINE config 5 -2.7%), not reliably at N = 5120 (-6% to
+// +1.4%).  A is e4m3 whatever the weight's format.
 static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
-  if (b_fmt != MXGG_FMT_E4M3 || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
+  if ((b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1) || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
   if (M / 2 > INT32_MAX || K >= (1 << 22)) return 0;
   return (size_t)M * (size_t)staged_ld(K) + 256;
 }

@@ -237,8 +237,9 @@ size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
  * Workspace bytes, on top of mxgg_grouped_mm_workspace_size, with which
  * mxgg_grouped_mm stages e4m3 operands in row pairs, or 0 where the copies
  * would not pay for themselves: B (E * N * K rounded up to 64, plus 256) for
- * E <= M / 8192 and K >= 4096, or K >= 2048 with N >= 4096; A (M * K rounded
- * up to 64, plus 256) for N >= 8192, K >= 2048 and M even.  The copies then
+ * E <= M / 8192 and K >= 4096, or K >= 2048 with N >= 4096 (e4m3 B only); A
+ * (M * K rounded up to 64, plus 256) for N >= 8192, K >= 2048 and M even
+ * (e4m3 or e2m1 B).  The copies then
  * cost a few percent of the GEMM's time and save more.  No counterpart in the
  * reference, whose Triton kernel reads its operands where they lie.
  */

@@ -134,7 +134,8 @@ def test_grouped_mm_workspace_without_gpu():
     assert lib.mxgg_grouped_mm_staging_size(8, 16641, 8192, 5120, E4M3) == 0                  # odd M
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 1024, E4M3) == 0     # K < 2048
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8191, 8192, E4M3) == 0     # odd N: no row pairs
-    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8192, E2M1) == 0     # e4m3 operands only
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8192, E2M1) == 16640 * 8192 + 256   # A only
+    assert lib.mxgg_grouped_mm_staging_size(1, 16640, 4096, 8192, E2M1) == 0     # an e2m1 weight is not staged
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8200, E4M3) == 0     # K % 32
     # wgrad: both operands, (N + K) * M rounded up to 64, plus 512; not for N + K < 10240 with
     # E * (N + K) <= 8192, odd N or K, or M off the 32 grid

@@ -324,6 +324,46 @@ def test_fwd_staged_weight_bitwise(gpu, case):
         assert torch.equal(ws[dst:dst + want.numel()], want)
 
 
+def test_fwd_staged_activations_beside_e2m1_weight(gpu):
+    """With an e2m1 weight (not staged) and N >= 8192, A alone is staged in
+    row pairs: same bits as the unstaged call, staged bytes as documented."""
+    import kernels
+    from kernels import _lib
+    lib = _lib.load()
+    E, M, N, K = 2, 4096, 8192, 2080
+    stage = lib.mxgg_grouped_mm_staging_size(E, M, N, K, _lib.FMT_E2M1)
+    ldp = (K + 63) // 64 * 64
+    assert stage == M * ldp + 256
+    offs = _odd_offs(E, M - 40, 17)
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    a = _x((M, K), 31, gpu)
+    w = _x((E, N, K), 32, gpu, 0.05)
+    sa, qa = kernels.to_mx(a)
+    sw, qw = kernels.to_mx(w, elem_dtype=torch.float4_e2m1fn_x2)
+    full = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
+    outs, wss = [], []
+    for ws_bytes in (full, full + stage):
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=gpu)
+        print(f"fwd e2m1 staged E={E} M={M} N={N} K={K} ws={ws_bytes}", flush=True)
+        _lib.check(lib.mxgg_grouped_mm(_u8(qa).data_ptr(), qa.stride(0), _u8(sa).data_ptr(), sa.stride(0),
+                                       _u8(qw).data_ptr(), _lib.FMT_E2M1, qw.stride(1), qw.stride(0),
+                                       _u8(sw).data_ptr(), sw.stride(1), sw.stride(0), o.data_ptr(), E, M, N, K,
+                                       out.data_ptr(), 0, out.stride(0), 0, 0, 0, 0, ws.data_ptr(), ws_bytes,
+                                       torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        outs.append(out)
+        wss.append(ws)
+    rows = int(offs[-1])
+    assert torch.equal(outs[1][:rows].view(torch.uint8), outs[0][:rows].view(torch.uint8))
+    ws = wss[1]
+    dst = (ws.data_ptr() + full + 255) // 256 * 256 - ws.data_ptr()
+    want = torch.zeros((M, ldp), dtype=torch.uint8, device=gpu)
+    want[:, :K] = _u8(qa)
+    want = want.view(M // 2, 2, ldp // 64, 64).permute(0, 2, 1, 3).reshape(-1)
+    assert torch.equal(ws[dst:dst + want.numel()], want)
+
+
 def test_fwd_drop_in_stages_the_weight(gpu):
     """The Python drop-in call on plain scales asks for the staging room
     (benchmark shape E=1, N=2048, K=8192): same bits as the step-scale call."""
