@@ -1848,6 +1848,7 @@ int launch_relayout(const ScaleJob& a, const ScaleJob& b, hipStream_t st, const 
   js.d2 = d2 ? *d2 : PairJob{};
   const int64_t grid = t01 + js.tiles_d + (d2 ? (int64_t)d2->batches * d2->pairs : 0);
   if (grid <= 0) return MXGG_OK;
+  if (grid > (int64_t)(UINT32_MAX / 256)) return fail(MXGG_ERR_UNSUPPORTED, "%s: re-layout grid too large", what);
   if (grid > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "%s: scale re-layout grid too large", what);
   hipLaunchKernelGGL(scale_relayout_kernel, dim3((unsigned)grid), dim3(256), 0, st, js);
   return launch_status(what);
@@ -1948,7 +1949,7 @@ static int64_t staged_ld(int64_t K) { return (K + 63) / 64 * 64; }
 static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
   if (b_fmt != MXGG_FMT_E4M3 || E <= 0 || N <= 0 || N % 2 || (int64_t)E * 8192 > M) return 0;
   if (K < 2048 || (K < 4096 && N < 4096)) return 0;
-  if ((int64_t)E * (N / 2) > INT32_MAX || K >= (1 << 22)) return 0;   // launch grid, int offsets
+  if ((int64_t)E * (N / 2) > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
   return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
 }
 
@@ -1960,7 +1961,7 @@ static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fm
 // +1.4%).  A is e4m3 whatever the weight's format.
 static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
   if ((b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1) || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
-  if (M / 2 > INT32_MAX || K >= (1 << 22)) return 0;
+  if (M / 2 > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
   return (size_t)M * (size_t)staged_ld(K) + 256;
 }
 
@@ -1975,7 +1976,7 @@ static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
 static size_t wgrad_staging_bytes(int E, int64_t M, int64_t N, int64_t K) {
   if (E <= 0 || M <= 0 || M % 32 || N <= 0 || K <= 0 || N % 2 || K % 2) return 0;
   if (N + K < 10240 && (int64_t)E * (N + K) <= 8192) return 0;
-  if (M >= (1 << 22) || (N / 2) > INT32_MAX || (K / 2) > INT32_MAX) return 0;   // int offsets, launch grid
+  if (M >= (1 << 22) || N / 2 + K / 2 > (1 << 22)) return 0;   // int offsets, launch grid
   return (size_t)(N + K) * (size_t)staged_ld(M) + 512;
 }
 
