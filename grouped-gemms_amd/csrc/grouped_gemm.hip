@@ -922,7 +922,7 @@ struct PairJob {
 struct ScaleJobs {
   ScaleJob j[2];
   int tiles0;                    // workgroups of job 0 (job 1 follows)
-  int tiles01;                   // workgroups of jobs 0 and 1 (the pair job follows)
+  int tiles01;                   // workgroups of jobs 0 and 1 (pair job d follows)
   PairJob d;
   int tiles_d;                   // workgroups of pair job d (pair job d2 follows)
   PairJob d2;
