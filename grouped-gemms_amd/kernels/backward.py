@@ -6,7 +6,9 @@ dim-1 quantized operands ``go_t (N, M)`` and ``ia_t (K, M)`` (scales per 32
 tokens), one reduction over each group's token range, output ``(E, N, K)``.
 As in the reference the stored values are rounded to bf16 whatever
 ``out_dtype`` is (backward.py:103, 214) and an empty group yields zeros.
-Step-major int32 scales (``(T, N)`` and ``(T, K)``, ``T = cdiv(M, 128)``, as
+On plain scales the call's re-layout launch also copies both operands into
+row pairs where the GEMM gains more than the copy costs
+(``mxgg_wgrad_staging_size``; same bits).  Step-major int32 scales (``(T, N)`` and ``(T, K)``, ``T = cdiv(M, 128)``, as
 ``to_mx_dim0(..., scale_layout="steps")`` writes them) skip the per-call
 re-layout (``mxgg_wgrad_steps``); with them either operand may be in row pairs
 (the view ``(N/2, 2, cdiv(M, 64), 64)``, resp. ``(K/2, ...)``, that

@@ -4,10 +4,12 @@ Drop-in for kernels/forward.py:461-606 of the reference: same name,
 positional order, defaults and return value.  ``output[s:e] = A[s:e] @ B[g]^T``
 per expert group, MX scales per 32 elements of K, fp32 accumulation, one
 rounding to ``out_dtype``.  The work runs in the hand-written HIP kernels of
-libmxgg (``mxgg_grouped_mm``): a scale re-layout launch, then the GEMM, which
-builds the expert->tile routing inside the kernel from ``group_end_offsets``
-(no host sync), and, when the last round of tiles is split along K, the
-piece and reduce launches.
+libmxgg (``mxgg_grouped_mm``): a scale re-layout launch (which also copies an
+e4m3 weight and / or the activations into row pairs where the GEMM gains more
+than the copy costs, ``mxgg_grouped_mm_staging_size``; same bits), then the
+GEMM, which builds the expert->tile routing inside the kernel from
+``group_end_offsets`` (no host sync), and, when the last round of tiles is
+split along K, the piece and reduce launches.
 
 Beyond the reference, the weight may be MXFP4: ``weight`` of dtype
 ``torch.float4_e2m1fn_x2`` (or uint8) with last dim K/2, two e2m1 values per
