@@ -6,14 +6,17 @@
 // swept M.  Fields: E, M, N, K, b_fmt (0 e4m3, 4 e2m1), block_m, block_n,
 // group_m, xcd swizzle, split (1: the last round may be split along K when
 // the workspace allows it, 0: whole tiles only).
-// sweep: 9 shapes (e4m3, 3 offset draws), 7 with a gain of at least 2% on every draw; AMD Radeon Graphics
+// sweep: 18 shapes (e4m3, 3 offset draws), 10 with a gain of at least 2% on every draw; AMD Radeon Graphics
 static const TunedFwd kTunedFwd[] = {
-    {1, 16640, 2048, 2048, 0, 256, 256, 1, 8, 0},   // 97.7 us
-    {1, 16640, 2048, 8192, 0, 256, 256, 4, 1, 1},   // 280.9 us
-    {1, 16640, 5120, 2048, 0, 256, 256, 4, 1, 0},   // 194.6 us
-    {1, 16640, 5120, 5120, 0, 256, 256, 4, 1, 0},   // 446.7 us
-    {1, 16640, 5120, 8192, 0, 256, 256, 8, 8, 1},   // 651.0 us
-    {1, 16640, 8192, 2048, 0, 256, 256, 4, 8, 1},   // 294.8 us
-    {1, 16640, 8192, 8192, 0, 256, 256, 16, 8, 1},   // 983.4 us
+    {1, 16640, 2048, 2048, 0, 256, 256, 1, 8, 1},   // 95.3 us
+    {1, 16640, 2048, 8192, 0, 256, 256, 4, 1, 1},   // 262.8 us
+    {1, 16640, 5120, 5120, 0, 256, 256, 4, 1, 1},   // 417.1 us
+    {1, 16640, 5120, 8192, 0, 256, 256, 8, 8, 0},   // 636.2 us
+    {1, 16640, 8192, 2048, 0, 256, 256, 1, 1, 0},   // 285.7 us
+    {1, 16640, 8192, 5120, 0, 256, 256, 4, 8, 1},   // 624.3 us
+    {1, 16640, 8192, 8192, 0, 256, 256, 4, 8, 1},   // 956.5 us
+    {2, 16640, 2048, 8192, 0, 256, 256, 4, 1, 1},   // 273.2 us
+    {2, 16640, 8192, 2048, 0, 256, 256, 1, 1, 1},   // 291.8 us
+    {2, 16640, 8192, 5120, 0, 256, 256, 1, 1, 0},   // 636.3 us
     {0, 0, 0, 0, 0, 0, 0, 0, 0, 0},   // end
 };

@@ -2,8 +2,9 @@
 
 Counterpart of the reference's tune_worker.py (tune_worker.py:21-109): one
 (E, M, N, K) problem, every launch configuration libmxgg has built, each timed
-as the median device time of a ``mxgg_grouped_mm`` call (scale re-layout,
-GEMM, and the piece / reduce launches of a split last round) with the caches
+as the median device time of a ``mxgg_grouped_mm`` call (scale re-layout
+with the operand staging the drop-in call makes, GEMM, and the piece /
+reduce launches of a split last round) with the caches
 flushed before every repetition.  The search space is the set of built
 instantiations rather than Triton meta-parameters:
 
@@ -99,7 +100,9 @@ def sweep(E: int, M: int, N: int, K: int, fmt: str = "e4m3", limit: int | None =
     out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     full = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
     scales_only = 4 * ((K + 127) // 128) * (M + E * N)
-    ws = torch.empty(max(full, 1), dtype=torch.uint8, device=dev)
+    # plus the operand staging the drop-in call makes (it keeps the split room)
+    stage = lib.mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt)
+    ws = torch.empty(max(full + stage, 1), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
 
     def call(cfg, ws_bytes, offs):
@@ -128,7 +131,7 @@ def sweep(E: int, M: int, N: int, K: int, fmt: str = "e4m3", limit: int | None =
             os.replace(tmp, out_path)
 
     for i, cfg in enumerate(cfgs):
-        ws_bytes = full if cfg["SPLIT"] else scales_only
+        ws_bytes = (full if cfg["SPLIT"] else (scales_only + 255) // 256 * 256) + stage
         try:
             ts = [float(benchmark_cuda_function_in_microseconds(call, cfg, ws_bytes, o, warmup_ms=10.0,
                                                                 rep_ms=rep_ms)) for o in offs_list]
