@@ -33,8 +33,14 @@ region): kernel-only time again, reported as ``native_geomean_tflops`` and
 training step (forward + backward) of the MoE layer (kernels/moe.py) and one
 GPU's share of the sweep under 8-way expert parallelism (E=1, M=2080).
 
-Prints ONE JSON line on stdout; progress and the per-shape table go to stderr
-and to gpurun_out/bench_detail.json when that directory exists.
+CPU baseline (``cpu_baseline``): the reference's CPU path -- torch to_mx on
+the host, dequantize, one fp32 torch.matmul per group -- on BASELINE config 1
+at full size with torch's intra-op threads, beside the GPU drop-in time of the
+same quantized operands.
+
+Prints ONE JSON line on stdout, with the per-shape medians of the sweep in its
+``rows`` field; progress and the per-shape table also go to stderr and to
+gpurun_out/bench_detail.json when that directory exists.
 """
 
 from __future__ import annotations
@@ -364,39 +370,75 @@ def geomean(xs):
     return math.exp(sum(math.log(x) for x in xs) / len(xs))
 
 
-def cpu_baseline(budget_s: float):
-    """Oracle CPU path (dequantize -> per-group fp32 matmul -> bf16) on a bounded
-    sample of the workload: the forward of BASELINE config 2's shape family
-    (E=1, N=K=2048) on a row slice of M sized to about `budget_s` seconds."""
+def cpu_baseline(budget_s: float, dev, flush, steps: int, warmup: int):
+    """The reference's CPU path, timed on this host's cores beside the HIP path
+    on the same problem: BASELINE config 1 at full size (E=4, M=1024,
+    N=K=512, the config the reference's CPU-runnable pieces cover), quantized
+    on the CPU with the torch restatement of to_mx (utils.py:84-105; bits equal
+    to the GPU quantizer's), then dequantize -> one fp32 torch.matmul per
+    group -> bf16 with torch's intra-op threads (oracle/torch_ref.py), about
+    two thirds of `budget_s`.  `gpu_us` is the drop-in forward of the same
+    quantized operands on the GPU (median, same flush as the sweep).  The
+    numpy port of the oracle on a row slice of config 2's shape is kept as
+    `port_sample` for the rest of the budget."""
     import numpy as np
     import torch
     sys.path.insert(0, ROOT)
     from oracle import mx_oracle as O
+    from oracle import torch_ref as T
+    import kernels
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    rng = np.random.default_rng(1)
-    N = K = 2048
-    rows = 2048
-    a = rng.standard_normal((rows, K), dtype=np.float32)
-    b = (rng.standard_normal((1, N, K), dtype=np.float32) * 0.02).astype(np.float32)
-    sa, qa = O.to_mx(a, src="f32")
-    sb, qb = O.to_mx(b, src="f32")
-    offs = np.array([rows], dtype=np.int32)
-    flops = 2.0 * rows * N * K
-    t_total, reps = 0.0, 0
-    while t_total < budget_s or reps < 2:
+    threads = torch.get_num_threads()
+    E, M, N, K = 4, 1024, 512, 512
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    b = (torch.randn((E, N, K), generator=g) * 0.02).to(torch.bfloat16)
+    offs = [int(v) for v in O.generate_jagged_offs(E, M, 32, rng=random.Random(0))]
+    sa, qa = T.to_mx(a)
+    sb, qb = T.to_mx(b)
+    flops = 2.0 * M * N * K
+    # the HIP path on the same operands
+    da, dsa, db, dsb = (t.to(dev) for t in (qa, sa, qb, sb))
+    doffs = torch.tensor(offs, dtype=torch.int32, device=dev)
+    gpu_ms, _ = time_call(lambda: kernels.triton_mxfp8_grouped_mm(da, db, dsa, dsb, doffs), steps, warmup, flush)
+    gpu_out = kernels.triton_mxfp8_grouped_mm(da, db, dsa, dsb, doffs).cpu()
+    t_total, reps, out = 0.0, 0, None
+    while t_total < budget_s * 2 / 3 or reps < 3:
         t0 = time.perf_counter()
-        out = O.grouped_mm(qa, sa, qb, sb, offs, dtype=np.float32)
-        O.f32_to_bf16_bits(out)
+        out = T.grouped_mm(qa, sa, qb, sb, offs)
         t_total += time.perf_counter() - t0
         reps += 1
     per = t_total / reps
-    return {"value": round(flops / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+    agree = O.rel_fro(out.float().numpy(), gpu_out.float().numpy())
+
+    # the numpy port (oracle) on a slice of config 2's shape
+    rng = np.random.default_rng(1)
+    rows, N2 = 2048, 2048
+    a2 = rng.standard_normal((rows, N2), dtype=np.float32)
+    b2 = (rng.standard_normal((1, N2, N2), dtype=np.float32) * 0.02).astype(np.float32)
+    s2a, q2a = O.to_mx(a2, src="f32")
+    s2b, q2b = O.to_mx(b2, src="f32")
+    p_total, p_reps = 0.0, 0
+    while p_total < budget_s / 3 or p_reps < 2:
+        t0 = time.perf_counter()
+        O.f32_to_bf16_bits(O.grouped_mm(q2a, s2a, q2b, s2b, np.array([rows], np.int32), dtype=np.float32))
+        p_total += time.perf_counter() - t0
+        p_reps += 1
+    return {"value": round(flops / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "threads": threads,
             "kind": "port",
-            "sample": f"oracle fwd (dequantize e4m3+e8m0 -> fp32 matmul -> bf16), E=1, M={rows}, "
-                      f"N=K=2048, {reps} reps in {t_total:.1f}s, numpy/BLAS threads={threads}, "
-                      f"cpu={platform.processor() or platform.machine()}"}
+            "workload": "BASELINE config 1 at full size: E=4, M=1024, N=K=512, offs random.Random(0) "
+                        f"{offs}, e4m3 + e8m0 operands (torch to_mx on the CPU, utils.py:84-105)",
+            "sample": f"torch CPU path (dequantize -> per-group fp32 torch.matmul -> bf16, oracle/torch_ref.py), "
+                      f"{reps} reps in {t_total:.1f}s, torch threads={threads}, "
+                      f"cpu={platform.processor() or platform.machine()}, os.cpu_count={os.cpu_count()}",
+            "us": round(per * 1e6, 1),
+            "gpu_us": round(gpu_ms * 1e3, 2),
+            "gpu_tflops": round(flops / (gpu_ms * 1e-3) / 1e12, 2),
+            "gpu_over_cpu": round(per / (gpu_ms * 1e-3), 1),
+            "gpu_vs_cpu_rel_fro": round(agree, 6),
+            "port_sample": {"value": round(2.0 * rows * N2 * N2 / (p_total / p_reps) / 1e12, 5), "unit": "TFLOP/s",
+                            "sample": f"numpy oracle fwd (dequantize -> fp32 matmul -> bf16), E=1, M={rows}, "
+                                      f"N=K={N2}, {p_reps} reps in {p_total:.1f}s"}}
 
 
 NATIVE_TAG = " [row pairs]"
@@ -836,7 +878,7 @@ def main():
                                          "of a split last round")
     roofline_native = make_roofline(nstats, NATIVE_TAG, "the same launches on row-pair data (native layout)")
 
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_budget, dev, flush, args.steps, args.warmup)
     value = fwd_gm if fwd_gm is not None else (dgrad_gm or wgrad_gm)
     if value is None:            # --kernel-only / --native-only: no drop-in call was timed
         value = next((v for v in list(kernel_geomeans(rows, "_kernel_us").values()) +
@@ -888,6 +930,13 @@ def main():
         "roofline": roofline,
         "roofline_native": roofline_native,
         "cpu_baseline": cpu,
+        "rows": {"cols": ["E", "N", "K", "fwd_us", "dgrad_us", "wgrad_us", "fwd_native_us", "dgrad_native_us",
+                          "wgrad_native_us"],
+                 "what": "per sweep shape (M=16640): drop-in call medians, then kernel-only medians on the "
+                         "native layout (row pairs, step-major scales), microseconds",
+                 "data": [[r["E"], r["N"], r["K"]] + [round(r[c], 1) if c in r else None for c in
+                          ("fwd_us", "dgrad_us", "wgrad_us", "fwd_native_us", "dgrad_native_us", "wgrad_native_us")]
+                          for r in rows]},
         "wall_s": round(time.time() - t_start, 1),
     }
     outdir = os.path.join(ROOT, "gpurun_out")

@@ -704,6 +704,8 @@ __device__ __forceinline__ void edge_chunks(const Operand& X, const Operand& W, 
 template <bool BF16_ONLY>
 __device__ __forceinline__ void store4(uint8_t* out, int64_t ldo, int out_dtype, bool vec, int r, int c,
                                        int cols, float v0, float v1, float v2, float v3) {
+  // f32 and f16 outputs of BF16_ONLY hold the bf16-rounded value (f16:
+  // converted from it)
   if (out_dtype == MXGG_DTYPE_F32) {
     if (BF16_ONLY) {
       v0 = round_bf16(v0); v1 = round_bf16(v1); v2 = round_bf16(v2); v3 = round_bf16(v3);
@@ -723,6 +725,9 @@ __device__ __forceinline__ void store4(uint8_t* out, int64_t ldo, int out_dtype,
       w0 = pack_bf16x2(v0, v1);
       w1 = pack_bf16x2(v2, v3);
     } else {
+      if (BF16_ONLY) {
+        v0 = round_bf16(v0); v1 = round_bf16(v1); v2 = round_bf16(v2); v3 = round_bf16(v3);
+      }
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       h2 a = {(_Float16)v0, (_Float16)v1}, b = {(_Float16)v2, (_Float16)v3};
       w0 = __builtin_bit_cast(uint32_t, a);
@@ -810,8 +815,9 @@ constexpr int store_pass_rows(int fm, int lim) {
 }
 
 // BF16: the 16-bit output type (bf16, else f16), fixed at compile time so the
-// staging loop carries no per-write type test.
-template <class C, bool BF16>
+// staging loop carries no per-write type test.  RB16 (f16 only): convert the
+// bf16-rounded value (the weight gradient's store semantics).
+template <class C, bool BF16, bool RB16 = false>
 __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], uint8_t* smem,
                                                uint8_t* out, int64_t ldo, int rows, int cols) {
   constexpr int RB = C::WTN * 2;                 // staged row bytes
@@ -843,8 +849,12 @@ __device__ __forceinline__ void store_tile_lds(const v16f (&acc)[C::FM][C::FN], 
             w1 = pack_bf16x2(a[4 * q4 + 2], a[4 * q4 + 3]);
           } else {
             typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            h2 x = {(_Float16)a[4 * q4 + 0], (_Float16)a[4 * q4 + 1]};
-            h2 y = {(_Float16)a[4 * q4 + 2], (_Float16)a[4 * q4 + 3]};
+            float f0 = a[4 * q4 + 0], f1 = a[4 * q4 + 1], f2 = a[4 * q4 + 2], f3 = a[4 * q4 + 3];
+            if constexpr (RB16) {
+              f0 = round_bf16(f0); f1 = round_bf16(f1); f2 = round_bf16(f2); f3 = round_bf16(f3);
+            }
+            h2 x = {(_Float16)f0, (_Float16)f1};
+            h2 y = {(_Float16)f2, (_Float16)f3};
             w0 = __builtin_bit_cast(uint32_t, x);
             w1 = __builtin_bit_cast(uint32_t, y);
           }
@@ -1554,9 +1564,15 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
   }
   if constexpr (EPI == kEpiBf16) {
     store_tile_lds<C, true>(acc, smem, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * 2, p.K, rows, cols);
-  } else {   // f32, or bf16 rows off the 16-byte grid
-    const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-    store_tile<C, true>(acc, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz, p.K, rows, cols, p.out_dtype);
+  } else if constexpr (EPI == kEpiF16) {   // f16 of the bf16-rounded value
+    store_tile_lds<C, false, true>(acc, smem, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * 2, p.K, rows,
+                                   cols);
+  } else if constexpr (EPI == kEpiF16Any) {   // the same, rows off the 16-byte grid
+    store_tile<C, true>(acc, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * 2, p.K, rows, cols, MXGG_DTYPE_F16);
+  } else {   // f32, or bf16 rows off the 16-byte grid (the type known to be one of the two)
+    const int dt = p.out_dtype == MXGG_DTYPE_F32 ? MXGG_DTYPE_F32 : MXGG_DTYPE_BF16;
+    const int esz = dt == MXGG_DTYPE_F32 ? 4 : 2;
+    store_tile<C, true>(acc, p.out + ((int64_t)g * p.N * p.K + n0 * p.K + k0) * esz, p.K, rows, cols, dt);
   }
 }
 
@@ -1638,6 +1654,43 @@ __global__ __launch_bounds__(64) void schedule_kernel(FwdParams p, int programs,
 
 using namespace mxgg;
 
+// Row stride of a weight staged in row pairs (K bytes rounded up to 64).
+static int64_t staged_ld(int64_t K) { return (K + 63) / 64 * 64; }
+
+// Extra workspace for staging an e4m3 weight in row pairs, or 0 where the
+// call would not gain from it.  Staging copies the weight once (2 E N K
+// bytes of HBM traffic in the re-layout launch the call makes anyway); the
+// GEMM then copies whole 128-byte lines of it.  Measured over the sweep
+// shapes (MI355X, M = 16640, whole drop-in calls): E = 1 and 2 gain 2-10%
+// at K >= 5120 and 2-3% at K = 2048 with N >= 5120 (nothing at N = K = 2048);
+// E = 4 gains on some shapes and loses up to 3% on others: the copy's time
+// over the GEMM's is about 400 E / M (5 TB/s against 2 PFLOP/s), so
+// E <= M / 8192.  256 bytes of slack keep the staged lines 256-byte aligned.
+static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
+  if (b_fmt != MXGG_FMT_E4M3 || E <= 0 || N <= 0 || N % 2 || (int64_t)E * 8192 > M) return 0;
+  if (K < 2048 || (K < 4096 && N < 4096)) return 0;
+  if ((int64_t)E * (N / 2) > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
+  return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
+}
+
+// The same for A (M, K), or 0: its copy's time over the GEMM's is about
+// 400 / N, and staging it paid at N >= 8192 on every sweep shape (drop-in
+// call, same box: -1 to -12% at E = 4 and 8, where the weight is not staged;
+// -0.1 to -6% at E = 1 and 2 on top of the staged weight; with e2m1
+// weights, BASELINE config 5 -2.7%), not reliably at N = 5120 (-6% to
+// +1.4%).  A is e4m3 whatever the weight's format.
+static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
+  if ((b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1) || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
+  if (M / 2 > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
+  return (size_t)M * (size_t)staged_ld(K) + 256;
+}
+
+// Operand layout (MXGG_A_PAIRS / MXGG_B_PAIRS) of a plain-scale forward call
+// given the workspace for its staging (mxgg_grouped_mm_staging_size).
+static int dropin_layout(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
+  return (fwd_staging_bytes(E, M, N, K, b_fmt) ? MXGG_B_PAIRS : 0) | (fwd_staging_bytes_a(M, N, K, b_fmt) ? MXGG_A_PAIRS : 0);
+}
+
 namespace {
 
 typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_256;
@@ -1660,11 +1713,15 @@ struct TunedFwd {
 
 #include "tuned_fwd.h"
 
-// Tuned entry for (E, M, N, K, b_fmt): same E, N, K and format, M within a
-// factor of two of the swept M; null when the sweep did not cover the shape.
-const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
+// Tuned entry for (E, M, N, K, b_fmt) on operand layout `layout`: same E,
+// N, K and format, M within a factor of two of the swept M, and the operand
+// layout the sweep timed -- that of the drop-in call at the swept shape, with
+// its operands staged by the library's rule (dropin_layout) -- since the best
+// launch differs between layouts; null otherwise.
+const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int layout) {
   for (const TunedFwd* t = kTunedFwd; t->E; ++t)
-    if (t->E == E && t->N == N && t->K == K && t->b_fmt == b_fmt && 2 * M >= t->M && M <= 2 * (int64_t)t->M)
+    if (t->E == E && t->N == N && t->K == K && t->b_fmt == b_fmt && 2 * M >= t->M && M <= 2 * (int64_t)t->M &&
+        layout == dropin_layout(t->E, t->M, t->N, t->K, t->b_fmt))
       return t;
   return nullptr;
 }
@@ -1681,11 +1738,11 @@ const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
 template <class C>
 int fwd_resident();
 
-FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, int bn, int gm,
+FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int layout, int bm, int bn, int gm,
                    int xcd) {
   FwdChoice c{256, 256, 12, 8, true};
   const int64_t tiles256 = (cdiv(M, 256) + E - 1) * cdiv(N, 256);
-  if (const TunedFwd* t = find_tuned(E, M, N, K, b_fmt)) {
+  if (const TunedFwd* t = find_tuned(E, M, N, K, b_fmt, layout)) {
     c = FwdChoice{t->bm, t->bn, t->group_m, t->xcd, t->split != 0};
   } else if (b_fmt == MXGG_FMT_E4M3 && tiles256 < 128) {
     // Under half a chip of 256 x 256 tiles: 128 x 128 tiles (two per CU)
@@ -1934,37 +1991,6 @@ static size_t split_area(int64_t tiles, size_t tile_bytes, int64_t nsteps) {
   return want < (double)kSplitBytes ? (size_t)want : kSplitBytes;
 }
 
-// Row stride of a weight staged in row pairs (K bytes rounded up to 64).
-static int64_t staged_ld(int64_t K) { return (K + 63) / 64 * 64; }
-
-// Extra workspace for staging an e4m3 weight in row pairs, or 0 where the
-// call would not gain from it.  Staging copies the weight once (2 E N K
-// bytes of HBM traffic in the re-layout launch the call makes anyway); the
-// GEMM then copies whole 128-byte lines of it.  Measured over the sweep
-// shapes (MI355X, M = 16640, whole drop-in calls): E = 1 and 2 gain 2-10%
-// at K >= 5120 and 2-3% at K = 2048 with N >= 5120 (nothing at N = K = 2048);
-// E = 4 gains on some shapes and loses up to 3% on others: the copy's time
-// over the GEMM's is about 400 E / M (5 TB/s against 2 PFLOP/s), so
-// E <= M / 8192.  256 bytes of slack keep the staged lines 256-byte aligned.
-static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
-  if (b_fmt != MXGG_FMT_E4M3 || E <= 0 || N <= 0 || N % 2 || (int64_t)E * 8192 > M) return 0;
-  if (K < 2048 || (K < 4096 && N < 4096)) return 0;
-  if ((int64_t)E * (N / 2) > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
-  return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
-}
-
-// The same for A (M, K), or 0: its copy's time over the GEMM's is about
-// 400 / N, and staging it paid at N >= 8192 on every sweep shape (drop-in
-// call, same box: -1 to -12% at E = 4 and 8, where the weight is not staged;
-// -0.1 to -6% at E = 1 and 2 on top of the staged weight; with e2m1
-// weights, BASELINE config 5 -2.7%), not reliably at N = 5120 (-6% to
-// +1.4%).  A is e4m3 whatever the weight's format.
-static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
-  if ((b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1) || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
-  if (M / 2 > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
-  return (size_t)M * (size_t)staged_ld(K) + 256;
-}
-
 // Extra workspace for staging both wgrad operands (go_t (N, M), ia_t (K, M))
 // in row pairs, or 0 where that would not pay.  The copy moves 2 (N + K) M
 // bytes in the scale re-layout launch; the GEMM then copies whole lines
@@ -1989,15 +2015,45 @@ extern "C" size_t mxgg_grouped_mm_staging_size(int E, int64_t M, int64_t N, int6
   return fwd_staging_bytes(E, M, N, K, b_fmt) + fwd_staging_bytes_a(M, N, K, b_fmt);
 }
 
+// Partial-tile room of a forward call: the most a split plan of the call can
+// use (256 x 256 or 128 x 128 tiles, whichever needs more).  Calls given more
+// use no more, so every call with at least this room makes the same plan.
+static size_t fwd_part_cap(int E, int64_t M, int64_t N, int64_t K) {
+  if (E <= 0 || M <= 0 || N <= 0 || K <= 0) return 0;
+  const int64_t nsteps = cdiv(K, STEP);
+  const size_t a = split_area((cdiv(M, 256) + E - 1) * cdiv(N, 256), (size_t)256 * 256 * 4, nsteps);
+  const size_t b = split_area((cdiv(M, 128) + E - 1) * cdiv(N, 128), (size_t)128 * 128 * 4, nsteps);
+  return a > b ? a : b;
+}
+
 extern "C" size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
   if (E <= 0 || M < 0 || N < 0 || K < 0) return 0;
   const size_t sc = fwd_scale_bytes(E, M, N, K);
   if (sc == 0 || M == 0 || N == 0) return sc;
-  const int64_t nsteps = cdiv(K, STEP);
-  const size_t a = split_area((cdiv(M, 256) + E - 1) * cdiv(N, 256), (size_t)256 * 256 * 4, nsteps);
-  const size_t b = split_area((cdiv(M, 128) + E - 1) * cdiv(N, 128), (size_t)128 * 128 * 4, nsteps);
-  const size_t part = a > b ? a : b;
+  const size_t part = fwd_part_cap(E, M, N, K);
   return part ? align256(sc) + part : sc;
+}
+
+// Where the parts of a caller's workspace go (plain-scale entry points): the
+// re-laid scales (`need` bytes) first; then, 256-byte aligned, the partial
+// tiles, given at most `cap` bytes; then, from the bytes past those, the
+// staged operands (`stage` bytes, carved from the end).  A workspace of the
+// recommended size therefore stages nothing, and a larger one stages without
+// taking room from the partial tiles: the split plan, and the bits, are those
+// of the unstaged call.
+struct WsLayout {
+  size_t part_off;    // first byte of the partial area
+  size_t part;        // its bytes (0: no tile is split)
+  size_t extra;       // bytes past the scales and the partial area
+};
+
+static WsLayout ws_layout(size_t ws_bytes, size_t need, size_t cap) {
+  WsLayout w{align256(need), 0, 0};
+  const size_t avail = ws_bytes > w.part_off ? ws_bytes - w.part_off : 0;
+  w.part = avail < cap ? avail : cap;
+  const size_t used = w.part ? w.part_off + w.part : need;
+  w.extra = ws_bytes > used ? ws_bytes - used : 0;
+  return w;
 }
 
 // Bytes a row of `len` bytes takes in an operand stored in pieces of `piece`
@@ -2061,7 +2117,7 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
                              int64_t ldb_n, int64_t ldb_e, const uint8_t* bs, const int32_t* offs, int E, int64_t M,
                              int64_t N, int64_t K, void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
                              int group_m, int xcd, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
-  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
+  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, layout, block_m, block_n, group_m, xcd);
   const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
                                            : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
   if (!built) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built", c.bm, c.bn);
@@ -2070,7 +2126,11 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
   FwdParams p{A, lda, B, ldb_n, ldb_e, as, (uint32_t)(4 * T * M), bs, (uint32_t)(4 * T * N), offs, E, M, N, K,
               (uint8_t*)out, out_dtype, ldo, 0, 0, 0, part, 0, 0, 0,
               (layout & MXGG_A_PAIRS) ? 1 : 0, (layout & MXGG_B_PAIRS) ? 1 : ((layout & MXGG_B_QUADS) ? 2 : 0)};
-  const size_t pb = part ? part_bytes : 0;
+  // no more room than the split plans of this shape can use (ws_layout)
+  const size_t cap = fwd_part_cap(E, M, N, K);
+  const size_t pb = part ? (part_bytes < cap ? part_bytes : cap) : 0;
+  if (!pb) part = nullptr;
+  p.part = part;
   if (b_fmt == MXGG_FMT_E2M1)
     return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
   if (c.bm == 256)
@@ -2090,39 +2150,32 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
   hipStream_t st = (hipStream_t)stream;
   const int64_t T = cdiv(K, STEP);
   uint32_t* wsd = (uint32_t*)workspace;
-  const size_t part_off = align256(need);
-  size_t room = ws_bytes > part_off ? ws_bytes - part_off : 0;
+  const WsLayout wl = ws_layout(ws_bytes, need, fwd_part_cap(E, M, N, K));
   // The weight, then A, in row pairs, staged at the end of the workspace
-  // (the weight last) when it has room for them on top of the partial tiles
-  // (which keep the room they would have without them: the same split plan,
-  // the same bits).
+  // (the weight last) from the bytes past the partial area (ws_layout).
   const size_t stage_b = fwd_staging_bytes(E, M, N, K, b_fmt), stage_a = fwd_staging_bytes_a(M, N, K, b_fmt);
   const int ldp = (int)staged_ld(K);
+  // (each staging size holds 256 bytes of slack for aligning its start)
+  uint8_t* const end = (uint8_t*)workspace + ws_bytes;
   PairJob pb{}, pa{};
-  const bool staged_b = T > 0 && stage_b && room >= stage_b;
-  if (staged_b) {
-    room -= stage_b;
-    uint8_t* dst = (uint8_t*)align256((size_t)((uint8_t*)workspace + part_off + room));
-    pb = PairJob{B, ldb_n, ldb_e, dst, ldp, (int)(N / 2), E, (int)K};
-  }
-  const bool staged_a = T > 0 && stage_a && room >= stage_a;
-  if (staged_a) {
-    room -= stage_a;
-    uint8_t* dst = (uint8_t*)align256((size_t)((uint8_t*)workspace + part_off + room));
-    pa = PairJob{A, lda, 0, dst, ldp, (int)(M / 2), 1, (int)K};
-  }
+  const bool staged_b = T > 0 && stage_b && wl.extra >= stage_b;
+  if (staged_b) pb = PairJob{B, ldb_n, ldb_e, (uint8_t*)align256((size_t)(end - stage_b)), ldp, (int)(N / 2), E, (int)K};
+  const size_t used_b = staged_b ? stage_b : 0;
+  const bool staged_a = T > 0 && stage_a && wl.extra >= used_b + stage_a;
+  if (staged_a)
+    pa = PairJob{A, lda, 0, (uint8_t*)align256((size_t)(end - used_b - stage_a)), ldp, (int)(M / 2), 1, (int)K};
   if (T > 0) {
     if (int rc = launch_relayout(scale_job(A_s, ldas, 0, wsd, M, 1, K / 32, T),
                                  scale_job(B_s, ldbs_n, ldbs_e, wsd + T * M, N, E, K / 32, T), st, "grouped_mm",
                                  staged_b ? &pb : nullptr, staged_a ? &pa : nullptr))
       return rc;
   }
-  void* part = room ? (void*)((uint8_t*)workspace + part_off) : nullptr;
+  void* part = wl.part ? (void*)((uint8_t*)workspace + wl.part_off) : nullptr;
   return launch_grouped_mm(staged_a ? pa.dst : A, staged_a ? (int64_t)ldp : lda, (const uint8_t*)wsd,
                            staged_b ? pb.dst : B, b_fmt, staged_b ? (int64_t)ldp : ldb_n,
                            staged_b ? N * ldp : ldb_e, (const uint8_t*)(wsd + T * M), offs, E, M, N, K, out,
                            out_dtype, ldo, block_m, block_n, group_m, xcd,
-                           (staged_b ? MXGG_B_PAIRS : 0) | (staged_a ? MXGG_A_PAIRS : 0), part, room, st);
+                           (staged_b ? MXGG_B_PAIRS : 0) | (staged_a ? MXGG_A_PAIRS : 0), part, wl.part, st);
 }
 
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,
@@ -2238,7 +2291,8 @@ extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, in
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_config: null output pointer");
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_config: weight format %d not E4M3/E2M1", b_fmt);
-  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, *block_m, *block_n, *group_m, *xcd_swizzle);
+  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, dropin_layout(E, M, N, K, b_fmt), *block_m, *block_n, *group_m,
+                         *xcd_swizzle);
   *block_m = c.bm;
   *block_n = c.bn;
   *group_m = c.group_m;
@@ -2260,14 +2314,20 @@ static int64_t wgrad_group_steps(int E, int64_t M) {
   return n > 0 ? n : 1;
 }
 
+// Partial-tile room of a wgrad call: the most its split plan can use.  With
+// several groups the kernels plan a lone under-filled round from the longest
+// group, which may hold all M tokens: room for that plan.
+static size_t wgrad_part_cap(int E, int64_t M, int64_t N, int64_t K) {
+  if (E <= 0 || M <= 0 || N <= 0 || K <= 0) return 0;
+  return split_area((int64_t)E * cdiv(N, 256) * cdiv(K, 256), (size_t)256 * 256 * 4,
+                    E > 1 ? cdiv(M, STEP) : wgrad_group_steps(E, M));
+}
+
 extern "C" size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K) {
   if (E <= 0 || M < 0 || N < 0 || K < 0) return 0;
   const size_t sc = wgrad_scale_bytes(M, N, K);
   if (sc == 0 || N == 0 || K == 0) return sc;
-  // With several groups the kernels plan a lone under-filled round from the
-  // longest group, which may hold all M tokens: room for that plan.
-  const size_t part = split_area((int64_t)E * cdiv(N, 256) * cdiv(K, 256), (size_t)256 * 256 * 4,
-                                 E > 1 ? cdiv(M, STEP) : wgrad_group_steps(E, M));
+  const size_t part = wgrad_part_cap(E, M, N, K);
   return part ? align256(sc) + part : sc;
 }
 
@@ -2277,8 +2337,8 @@ static int check_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, 
                        int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias, const int32_t* offs, int E, int64_t M,
                        int64_t N, int64_t K, const void* out, int out_dtype, bool plain, int layout, bool* empty) {
   *empty = false;
-  if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F32)
-    return fail(MXGG_ERR_INVALID_ARG, "wgrad: out_dtype %d not BF16/F32", out_dtype);
+  if (out_dtype != MXGG_DTYPE_BF16 && out_dtype != MXGG_DTYPE_F16 && out_dtype != MXGG_DTYPE_F32)
+    return fail(MXGG_ERR_INVALID_ARG, "wgrad: out_dtype %d not BF16/F16/F32", out_dtype);
   if (E <= 0 || E > 65535) return fail(MXGG_ERR_INVALID_ARG, "wgrad: E=%d out of range", E);
   if (M < 0 || N < 0 || K < 0) return fail(MXGG_ERR_INVALID_ARG, "wgrad: negative shape");
   if (M % 32) return fail(MXGG_ERR_INVALID_ARG, "wgrad: M=%lld must be a multiple of 32", (long long)M);
@@ -2315,6 +2375,9 @@ static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, c
                         int out_dtype, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
   typedef CfgF8_256 C;
   const int64_t T = cdiv(M, STEP);
+  // no more room than the split plans of this shape can use (ws_layout)
+  const size_t cap = wgrad_part_cap(E, M, N, K);
+  if (part_bytes > cap) part_bytes = cap;
   float* part = part_area && part_bytes ? (float*)part_area : nullptr;
   WgradParams p{go_t, ld_go, ia_t, ld_ia, gs, (uint32_t)(4 * T * N), is, (uint32_t)(4 * T * K), offs, E, M, N, K,
                 (uint8_t*)out, out_dtype, (int)cdiv(N, C::BM), (int)cdiv(K, C::BN), part, 0, 1, 0, 0, 0, 0,
@@ -2347,8 +2410,13 @@ static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, c
   const int64_t split_tiles_ub = p.dev ? tiles : (sp.units ? sp.units / sp.S : 0);
   if (whole_ub > 0) {
     const dim3 grid((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E);
-    if (out_dtype == MXGG_DTYPE_BF16 && K % 8 == 0 && (uintptr_t)out % 16 == 0)
+    const bool al16 = K % 8 == 0 && (uintptr_t)out % 16 == 0;
+    if (out_dtype == MXGG_DTYPE_BF16 && al16)
       hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiBf16>), grid, dim3(C::NT), 0, st, p);
+    else if (out_dtype == MXGG_DTYPE_F16 && al16)
+      hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiF16>), grid, dim3(C::NT), 0, st, p);
+    else if (out_dtype == MXGG_DTYPE_F16)
+      hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiF16Any>), grid, dim3(C::NT), 0, st, p);
     else
       hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiAny>), grid, dim3(C::NT), 0, st, p);
     if (int rc = launch_status("wgrad")) return rc;
@@ -2379,18 +2447,15 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
   hipStream_t st = (hipStream_t)stream;
   const int64_t T = cdiv(M, STEP);
   uint32_t* wsd = (uint32_t*)workspace;
-  const size_t part_off = align256(need);
-  size_t room = ws_bytes > part_off ? ws_bytes - part_off : 0;
-  // Both operands in row pairs, staged at the end of the workspace when it
-  // has room for them on top of the partial tiles (which keep the room they
-  // would have without it: the same split plan, the same bits).
+  const WsLayout wl = ws_layout(ws_bytes, need, wgrad_part_cap(E, M, N, K));
+  // Both operands in row pairs, staged at the end of the workspace from the
+  // bytes past the partial area (ws_layout; 512 bytes of slack align both).
   const size_t stage = wgrad_staging_bytes(E, M, N, K);
-  const bool staged = T > 0 && stage && room >= stage;
+  const bool staged = T > 0 && stage && wl.extra >= stage;
   PairJob pg{}, pi{};
   if (staged) {
-    room -= stage;
     const int ldp = (int)staged_ld(M);
-    uint8_t* dg = (uint8_t*)align256((size_t)((uint8_t*)workspace + part_off + room));
+    uint8_t* dg = (uint8_t*)align256((size_t)((uint8_t*)workspace + ws_bytes - stage));
     uint8_t* di = (uint8_t*)align256((size_t)(dg + (size_t)N * ldp));
     pg = PairJob{go_t, ld_go, 0, dg, ldp, (int)(N / 2), 1, (int)M};
     pi = PairJob{ia_t, ld_ia, 0, di, ldp, (int)(K / 2), 1, (int)M};
@@ -2401,10 +2466,10 @@ extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_
                                  staged ? &pg : nullptr, staged ? &pi : nullptr))
       return rc;
   }
-  void* part = room ? (void*)((uint8_t*)workspace + part_off) : nullptr;
+  void* part = wl.part ? (void*)((uint8_t*)workspace + wl.part_off) : nullptr;
   return launch_wgrad(staged ? pg.dst : go_t, staged ? (int64_t)pg.ld_dst : ld_go, (const uint8_t*)wsd,
                       staged ? pi.dst : ia_t, staged ? (int64_t)pi.ld_dst : ld_ia, (const uint8_t*)(wsd + T * N), offs,
-                      E, M, N, K, out, out_dtype, staged ? (MXGG_A_PAIRS | MXGG_B_PAIRS) : 0, part, room, st);
+                      E, M, N, K, out, out_dtype, staged ? (MXGG_A_PAIRS | MXGG_B_PAIRS) : 0, part, wl.part, st);
 }
 
 extern "C" int mxgg_wgrad_steps(const uint8_t* go_t, int64_t ld_go, const uint32_t* go_ss, const uint8_t* ia_t,

@@ -42,6 +42,16 @@ def _rowmajor(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _staging_enabled() -> bool:
+    """False when the environment sets ``MXGG_STAGING=0``: the drop-in calls
+    then allocate no room for copying operands into row pairs (less transient
+    memory per call -- up to E*N*K + M*K bytes for the forward, (N + K)*M for
+    wgrad -- at the cost of the GEMM reading row-major operands; the output
+    bits are the same).  Read per call."""
+    import os
+    return os.environ.get("MXGG_STAGING", "1") != "0"
+
+
 _OUT_CODES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16,
               torch.float32: _lib.DTYPE_F32}
 

@@ -5,10 +5,12 @@ Drop-in for kernels/backward.py:217-305 of the reference:
 dim-1 quantized operands ``go_t (N, M)`` and ``ia_t (K, M)`` (scales per 32
 tokens), one reduction over each group's token range, output ``(E, N, K)``.
 As in the reference the stored values are rounded to bf16 whatever
-``out_dtype`` is (backward.py:103, 214) and an empty group yields zeros.
-On plain scales the call's re-layout launch also copies both operands into
-row pairs where the GEMM gains more than the copy costs
-(``mxgg_wgrad_staging_size``; same bits).  Step-major int32 scales (``(T, N)`` and ``(T, K)``, ``T = cdiv(M, 128)``, as
+``out_dtype`` is (backward.py:101-104, 214, 251: float32 holds the bf16
+value, float16 the bf16 value converted to half) and an empty group yields
+zeros.  On plain scales the call's re-layout launch also copies both operands
+into row pairs where the GEMM gains more than the copy costs
+(``mxgg_wgrad_staging_size``; same bits; ``MXGG_STAGING=0`` in the
+environment leaves that room out).  Step-major int32 scales (``(T, N)`` and ``(T, K)``, ``T = cdiv(M, 128)``, as
 ``to_mx_dim0(..., scale_layout="steps")`` writes them) skip the per-call
 re-layout (``mxgg_wgrad_steps``); with them either operand may be in row pairs
 (the view ``(N/2, 2, cdiv(M, 64), 64)``, resp. ``(K/2, ...)``, that
@@ -20,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._common import _offsets, _out_code, _pair_geometry, _require, _rowmajor, _stream_handle, _u8
+from ._common import _offsets, _out_code, _pair_geometry, _require, _rowmajor, _staging_enabled, _stream_handle, _u8
 from .forward import _split_room
 
 
@@ -50,7 +52,8 @@ def triton_mxfp8_wgrad(
         BLOCK_N / BLOCK_K / BLOCK_M / num_warps / num_stages: accepted for
             signature compatibility; the HIP kernel uses its own tiling.
 
-    Returns ``(E, N, K)`` of ``out_dtype`` (bf16 or float32).
+    Returns ``(E, N, K)`` of ``out_dtype`` (bf16, float16 or float32), the
+    bf16-rounded products in each.
 
     Row-pair operands span M rounded up to 64; with both in row pairs that is
     the M used, which changes nothing: tokens past ``offs[-1]`` are in no
@@ -92,7 +95,7 @@ def triton_mxfp8_wgrad(
     ld_g = pg[2] if pg else g.stride(0)
     ld_a = pi[2] if pi else a.stride(0)
     offs = _offsets(group_end_offsets, dev)
-    code = _out_code(out_dtype, allowed=(torch.bfloat16, torch.float32))
+    code = _out_code(out_dtype)
     out = torch.empty((E, N, K), dtype=out_dtype, device=dev)
     lib = _lib.load()
     ws_bytes = lib.mxgg_wgrad_workspace_size(E, M, N, K)
@@ -109,8 +112,10 @@ def triton_mxfp8_wgrad(
         return out
     gs = _u8(_rowmajor(go_scale))
     as_ = _u8(_rowmajor(ia_scale))
-    # plus room to stage both operands in row pairs where that pays for its copy
-    ws_bytes += lib.mxgg_wgrad_staging_size(E, M, N, K)
+    # plus room to stage both operands in row pairs where that pays for its
+    # copy (none with MXGG_STAGING=0)
+    if _staging_enabled():
+        ws_bytes += lib.mxgg_wgrad_staging_size(E, M, N, K)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_wgrad(
         g.data_ptr(), g.stride(0), gs.data_ptr(), gs.stride(0),

@@ -9,7 +9,10 @@ e4m3 weight and / or the activations into row pairs where the GEMM gains more
 than the copy costs, ``mxgg_grouped_mm_staging_size``; same bits), then the
 GEMM, which builds the expert->tile routing inside the kernel from
 ``group_end_offsets`` (no host sync), and, when the last round of tiles is
-split along K, the piece and reduce launches.
+split along K, the piece and reduce launches.  The per-call workspace (torch's
+caching allocator) holds the re-laid scales, up to 128 MiB of fp32 partial
+tiles and the staged operands; ``MXGG_STAGING=0`` in the environment leaves
+the staging room out.
 
 Beyond the reference, the weight may be MXFP4: ``weight`` of dtype
 ``torch.float4_e2m1fn_x2`` (or uint8) with last dim K/2, two e2m1 values per
@@ -29,7 +32,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._common import _offsets, _out_code, _pair_geometry, _require, _rowmajor, _stream_handle, _u8
+from ._common import _offsets, _out_code, _pair_geometry, _require, _rowmajor, _staging_enabled, _stream_handle, _u8
 
 # Tile shapes built into libmxgg (BLOCK_M x BLOCK_N); BLOCK_K is fixed at 128.
 BUILT_TILES = ((256, 256), (128, 128))
@@ -185,8 +188,10 @@ def triton_mxfp8_grouped_mm(
         return out
     a_s = _u8(_rowmajor(input_act_scales))
     b_s = _u8(_rowmajor(weight_scales))
-    # plus room to stage the weight in row pairs where that pays for its copy
-    ws_bytes += lib.mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt)
+    # plus room to stage the weight and / or A in row pairs where that pays
+    # for its copy (none with MXGG_STAGING=0)
+    if _staging_enabled():
+        ws_bytes += lib.mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.mxgg_grouped_mm(
         a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),

@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MXGG_VERSION 4000 /* major*1000 + minor */
+#define MXGG_VERSION 4001 /* major*1000 + minor */
 
 /* status codes */
 #define MXGG_OK 0
@@ -193,7 +193,10 @@ int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t N, int blo
  * *xcd_swizzle on entry) are applied as mxgg_grouped_mm applies them; the
  * call returns MXGG_ERR_UNSUPPORTED when the resulting tile is not built.
  * Replaces `_pick_config` / `_BEST_CFGS` / `_FALLBACK_*`
- * (kernels/forward.py:399-459).
+ * (kernels/forward.py:399-459).  The answer is the one for a
+ * mxgg_grouped_mm call given room to stage its operands (the drop-in call):
+ * tuned entries apply only to calls on the operand layout they were timed
+ * on, so a *_steps call on another layout may get the built-in rule.
  */
 int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,
                            int* block_n, int* group_m, int* xcd_swizzle);
@@ -221,12 +224,15 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            mxgg_grouped_mm_workspace_size(E, M, N, K) bytes, which adds (after
  *            the scales, 256-byte aligned) room for the fp32 partial tiles of a
  *            last, partial round of tiles cut along K (at most 128 MiB; only for
- *            K >= 4096 and short launches).  With less, no tile is cut.  With
- *            mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt) bytes more, an
- *            e4m3 B and / or A is first copied into row pairs at the end of
- *            the workspace (in the scale re-layout launch), which the GEMM
- *            reads in whole 128-byte lines; the partial tiles keep the room
- *            they have without it, and the output bits are the same.
+ *            K >= 4096 and short launches).  With less, fewer or no tiles are
+ *            cut; more room than that is not used for partial tiles.  Bytes
+ *            past the scales and that partial room hold the staged operands:
+ *            with at least mxgg_grouped_mm_staging_size(E, M, N, K, b_fmt) of
+ *            them, an e4m3 B and / or A is first copied into row pairs at the
+ *            end of the workspace (in the scale re-layout launch), which the
+ *            GEMM reads in whole 128-byte lines.  A workspace of exactly the
+ *            recommended size stages nothing; staging never takes room from the
+ *            partial tiles, and the output bits are the same either way.
  * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
  * rows need no alignment.  Results do not depend on the workspace size beyond
  * fp32 summation order (a cut tile adds its pieces in a fixed order, so
@@ -278,8 +284,9 @@ int mxgg_grouped_mm_steps(const uint8_t* A, int64_t lda, const uint32_t* A_ss,
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid allocation).  Same arguments,
  * results and errors as mxgg_grouped_mm given a workspace of
- * MXGG_NOALLOC_SCRATCH_BYTES bytes (the weight staging included, where it
- * fits); the workspace is instead a device array
+ * MXGG_NOALLOC_SCRATCH_BYTES bytes (operands are staged only where the
+ * scales, the full partial room and the staging all fit in it); the
+ * workspace is instead a device array
  * inside this library, one per GPU, allocated when the library is loaded and
  * held until the process ends.  Calls it cannot take -- the re-laid scales,
  * 4 * ceil(K/128) * (M + E*N) bytes, above MXGG_NOALLOC_SCRATCH_BYTES -- are
@@ -300,25 +307,28 @@ int mxgg_grouped_mm_noalloc(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
  * Weight-gradient grouped GEMM: out[g] = GO[:, s:e] @ IA[:, s:e]^T, shape (E, N, K),
  * a reduction over each group's token range; an empty group gives zeros.
  * Replaces `triton_mxfp8_wgrad` (kernels/backward.py:217-305), including its
- * store of bf16-rounded values whatever out_dtype is (backward.py:103, 214).
+ * store of bf16-rounded values whatever out_dtype is (backward.py:101-104,
+ * 214, 251): f32 holds the bf16 value, f16 the bf16 value converted (RNE).
  *   go_t  (N, M) e4m3, row stride ld_go;   go_s (N, M/32), row stride ld_gos
  *   ia_t  (K, M) e4m3, row stride ld_ia;   ia_s (K, M/32), row stride ld_ias
  *   offs  (E,) int32 cumulative group ends, nondecreasing, offs[E-1] <= M.
  *         Any values: as in the reference (token masks by group, scales by
  *         token / 32), a 32-token scale block shared by two groups scales the
  *         tokens of both.
- *   out   (E, N, K) of out_dtype (BF16 or F32), contiguous
+ *   out   (E, N, K) of out_dtype (BF16, F16 or F32), contiguous
  *   workspace / ws_bytes: device scratch, need not be initialised.  Required:
  *         4 * ceil(M/128) * (N + K) bytes (the scales re-laid step-major);
  *         recommended: mxgg_wgrad_workspace_size(E, M, N, K), which adds room
  *         for the fp32 partial tiles of tiles cut along the token range when
  *         the tiles do not fill the chip (E = 1, or fewer tiles than
  *         resident workgroups; with E > 1 sized for a group of all M tokens,
- *         since the kernels cut by the longest group), at most 128 MiB.  With
- *         mxgg_wgrad_staging_size(E, M, N, K) bytes more, go_t and ia_t are
- *         first copied into row pairs at the end of the workspace (in the
- *         scale re-layout launch) and the GEMM reads whole 128-byte lines of
- *         them; the partial tiles keep their room, the output bits are the same.
+ *         since the kernels cut by the longest group), at most 128 MiB; more
+ *         is not used for partial tiles.  With mxgg_wgrad_staging_size(E, M,
+ *         N, K) bytes past the scales and that room, go_t and ia_t are first
+ *         copied into row pairs at the end of the workspace (in the scale
+ *         re-layout launch) and the GEMM reads whole 128-byte lines of them;
+ *         the recommended size alone stages nothing, the partial tiles keep
+ *         their room, and the output bits are the same either way.
  */
 size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 /*

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.mxgg_version() == 4000
+    assert lib.mxgg_version() == 4001
     assert isinstance(lib.mxgg_last_error_string(), bytes)
 
 
@@ -189,6 +189,43 @@ def test_wgrad_and_quant_validation_without_gpu():
     assert rc == _lib.ERR_INVALID_ARG and b"aligned" in lib.mxgg_last_error_string()
     rc = lib.mxgg_wgrad_steps(16, 48, 16, 16, 48, 16, 16, 1, 48, 8, 8, 16, 0, 0, None, 0, None)
     assert rc == _lib.ERR_INVALID_ARG and b"multiple of 32" in lib.mxgg_last_error_string()
+
+
+def test_wgrad_out_dtypes_without_gpu():
+    """wgrad takes bf16, f16 and f32 outputs (kernels/backward.py:251 allocates
+    any out_dtype): a valid f16 call passes every argument check and stops only
+    at the missing device; an unknown type code is rejected."""
+    from kernels import _lib
+    lib = _lib.load()
+    ws = 4 * 1 * (64 + 64)
+    for code in (_lib.DTYPE_BF16, _lib.DTYPE_F16, _lib.DTYPE_F32):
+        rc = lib.mxgg_wgrad(16, 64, 16, 2, 16, 64, 16, 2, 16, 1, 64, 64, 64, 16, code, 256, ws, None)
+        assert rc == _lib.ERR_NO_DEVICE, (code, lib.mxgg_last_error_string())
+    rc = lib.mxgg_wgrad(16, 64, 16, 2, 16, 64, 16, 2, 16, 1, 64, 64, 64, 16, 7, 256, ws, None)
+    assert rc == _lib.ERR_INVALID_ARG and b"out_dtype" in lib.mxgg_last_error_string()
+
+
+def test_noalloc_rejects_calls_beyond_the_array_without_gpu():
+    """mxgg_grouped_mm_noalloc rejects a call whose re-laid scales,
+    4 * cdiv(K, 128) * (M + E*N) bytes, exceed its device array with
+    MXGG_ERR_WORKSPACE, before anything is launched (the check precedes the
+    device lookup: a regression would return MXGG_ERR_NO_DEVICE here, never
+    launch).  Fake 16-byte-aligned pointers: nothing is dereferenced."""
+    from kernels import _lib
+    lib = _lib.load()
+    E, M, N, K = 8, 16640, 32768, 8192
+    assert 4 * (K // 128) * (M + E * N) > _lib.NOALLOC_SCRATCH_BYTES
+    p = 1 << 20
+    rc = lib.mxgg_grouped_mm_noalloc(p, K, p, K // 32, p, _lib.FMT_E4M3, K, N * K, p, K // 32, N * K // 32,
+                                     p, E, M, N, K, p, _lib.DTYPE_BF16, N, 0, 0, 0, 0, None)
+    assert rc == _lib.ERR_WORKSPACE
+    assert b"scratch" in lib.mxgg_last_error_string()
+    # one just inside the array passes the check and stops at the missing device
+    M2, N2, K2 = 4096, 4096, 2048
+    assert 4 * (K2 // 128) * (M2 + N2) <= _lib.NOALLOC_SCRATCH_BYTES
+    rc = lib.mxgg_grouped_mm_noalloc(p, K2, p, K2 // 32, p, _lib.FMT_E4M3, K2, N2 * K2, p, K2 // 32,
+                                     N2 * K2 // 32, p, 1, M2, N2, K2, p, _lib.DTYPE_BF16, N2, 0, 0, 0, 0, None)
+    assert rc == _lib.ERR_NO_DEVICE
 
 
 def test_row_pair_argument_checks():

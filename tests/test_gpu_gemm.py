@@ -245,18 +245,20 @@ def test_fwd_full_size_cfg2(gpu):
     assert sq.item() >= SQNR_GATE
 
 
-def test_fwd_full_size_cfg4_mxfp4(gpu):
-    """BASELINE config 4 at full size: E=8, M=16640, N=8192, K=5120, e4m3
+def test_fwd_full_size_cfg5_mxfp4(gpu):
+    """BASELINE config 5 at full size: E=8, M=16640, N=8192, K=5120, e4m3
     activations x packed e2m1 weights (jagged groups), against a GPU fp32
     dequantize -> per-group matmul of the same quantized operands.  The e2m1
     codes decode by the OCP MX table (sign bit 3, magnitudes 0 .. 6), element
-    2i in the low nibble."""
+    2i in the low nibble; that GPU reference is itself pinned to the oracle
+    (``grouped_mm(..., b_elem="e2m1")``, fp64) on 256 rows across a group
+    boundary x 128 columns, and so is the kernel's output there."""
     import random
 
     import kernels
     E, M, N, K = 8, 16640, 8192, 5120
     offs = O.generate_jagged_offs(E, M, 32, rng=random.Random(4))
-    print(f"cfg4 E={E} M={M} N={N} K={K} offs={offs}", flush=True)
+    print(f"cfg5 E={E} M={M} N={N} K={K} offs={offs}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(4)
     a = torch.randn((M, K), device=gpu, generator=g).to(torch.bfloat16)
     b = (torch.randn((E, N, K), device=gpu, generator=g) * 0.02).to(torch.bfloat16)
@@ -272,6 +274,8 @@ def test_fwd_full_size_cfg4_mxfp4(gpu):
     wd = (wv.reshape(E, N, K // 32, 32) * torch.exp2(sb.view(torch.uint8).float() - 127).unsqueeze(-1)).reshape(E, N, K)
     ad = (qa.float().reshape(M, K // 32, 32) * torch.exp2(sa.view(torch.uint8).float() - 127).unsqueeze(-1)).reshape(M, K)
     del wv
+    r0 = max(0, min(int(offs[0]) - 128, M - 256))   # rows r0 .. r0+255 straddle the first group end
+    ref_slice = torch.empty((256, 128), device=gpu)
     lo = 0
     err2 = ref2 = 0.0
     hp_err2 = hp2 = 0.0
@@ -285,8 +289,16 @@ def test_fwd_full_size_cfg4_mxfp4(gpu):
             hp = a[lo:hi].float() @ b[e].float().t()
             hp_err2 += (o - hp).square().sum().item()
             hp2 += hp.square().sum().item()
+            s0, s1 = max(lo, r0), min(hi, r0 + 256)
+            if s0 < s1:
+                ref_slice[s0 - r0:s1 - r0] = ref[s0 - lo:s1 - lo, :128]
         lo = hi
     assert (err2 / ref2) ** 0.5 <= REL_FRO_TIGHT
+    so = np.clip(np.asarray(offs, np.int64) - r0, 0, 256)
+    ora = O.grouped_mm(bits_u8(qa[r0:r0 + 256]), bits_u8(sa[r0:r0 + 256]), bits_u8(qb[:, :128]),
+                       bits_u8(sb[:, :128]), so, b_elem="e2m1")
+    assert O.rel_fro(ora, ref_slice.double().cpu().numpy()) <= 1e-4
+    assert O.rel_fro(ora, out[r0:r0 + 256, :128].float().cpu().numpy()) <= REL_FRO_TIGHT
     # fp4 weights lose more than fp8 against bf16: a sanity floor only
     assert 10 * torch.log10(torch.tensor(hp2 / hp_err2)).item() > 12.0
 
@@ -340,6 +352,25 @@ def test_wgrad_fp32_out_is_bf16_rounded(gpu):
     o = out.cpu()
     assert torch.equal(o, o.to(torch.bfloat16).float())
     _assert_close(f32(out), ref)
+
+
+@pytest.mark.parametrize("E,M,N,K,offs", [
+    (2, 512, 256, 256, [256, 512]),              # whole tiles, 16-byte rows: the LDS-staged f16 epilogue
+    (3, 1024, 320, 200, [100, 600, 1024]),       # K % 8 != 0: the per-element epilogue; bounds off the 32 grid
+    (1, 8192, 256, 512, [8192]),                 # E = 1, few tiles: pieces along the tokens and the reduce
+])
+def test_wgrad_fp16_out_is_bf16_converted(gpu, E, M, N, K, offs):
+    """out_dtype=float16: the reference allocates an fp16 output and its store
+    converts the bf16-rounded accumulator to it (kernels/backward.py:101-104,
+    251).  Bit for bit the same call's bf16 output converted to fp16 (torch's
+    RNE cast), on every epilogue path, and within tolerance of the oracle's
+    wgrad rounded to bf16 then fp16."""
+    out16, ref, _, _ = _wgrad_case(E, M, N, K, offs, gpu, seed=21, out_dtype=torch.float16)
+    outb, _, _, _ = _wgrad_case(E, M, N, K, offs, gpu, seed=21, out_dtype=torch.bfloat16)
+    assert out16.dtype == torch.float16
+    assert torch.equal(out16.view(torch.int16), outb.to(torch.float16).view(torch.int16))
+    want = torch.from_numpy(O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32)))).to(torch.float16)
+    _assert_close(f32(out16), want.double().numpy())
 
 
 @pytest.mark.parametrize("M,offs", [(1024, [16, 48, 1000, 1024]),          # 16- but not 32-aligned bounds

@@ -256,7 +256,7 @@ def _staged_call(qa, sa, qw, sw, offs_t, out_dtype, ws_bytes):
     a, a_s, b, b_s = _u8(qa), _u8(sa), _u8(qw), _u8(sw)
     code = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}[out_dtype]
     out = torch.full((M, N), float("nan"), dtype=out_dtype, device=qa.device)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=qa.device)
+    ws = torch.full((ws_bytes,), 0xA5, dtype=torch.uint8, device=qa.device)
     print(f"fwd staged E={E} M={M} N={N} K={K} out={out_dtype} ws={ws_bytes}", flush=True)
     _lib.check(lib.mxgg_grouped_mm(a.data_ptr(), a.stride(0), a_s.data_ptr(), a_s.stride(0),
                                    b.data_ptr(), 0, b.stride(1), b.stride(0),
@@ -299,7 +299,7 @@ def test_fwd_staged_weight_bitwise(gpu, case):
     sa, qa = kernels.to_mx(a)
     sw, qw = kernels.to_mx(w)
     full = lib.mxgg_grouped_mm_workspace_size(E, M, N, K)
-    plain, _ = _staged_call(qa, sa, qw, sw, o, out_dtype, full)
+    plain, ws0 = _staged_call(qa, sa, qw, sw, o, out_dtype, full)
     staged, ws = _staged_call(qa, sa, qw, sw, o, out_dtype, full + stage)
     rows = int(offs[-1])
     assert torch.equal(staged[:rows].view(torch.uint8), plain[:rows].view(torch.uint8))
@@ -316,6 +316,11 @@ def test_fwd_staged_weight_bitwise(gpu, case):
         want[..., :K] = _u8(qw)
         want = want.view(E, N // 2, 2, ldp // 64, 64).permute(0, 1, 3, 2, 4).reshape(-1)
         assert torch.equal(ws[dst:dst + want.numel()], want)
+        # the recommended size alone stages nothing: no copy of the weight where
+        # staging out of the partial room would have put it
+        d0 = (ws0.data_ptr() + full - stage_b + 255) // 256 * 256 - ws0.data_ptr()
+        if d0 >= 0:
+            assert not torch.equal(ws0[d0:d0 + want.numel()], want)
     if stage_a:
         dst = (end - stage_b - stage_a + 255) // 256 * 256 - ws.data_ptr()
         want = torch.zeros((M, ldp), dtype=torch.uint8, device=gpu)

@@ -458,3 +458,53 @@ def test_quantized_gemm_sqnr_matches_reference_level():
     out = O.grouped_mm(qa, sa, qb, sb, offs)
     hp = O.grouped_mm_hp(O.bf16_bits_to_f32(ab), O.bf16_bits_to_f32(bb), offs)
     assert 27.0 <= O.sqnr_db(hp, out) <= 28.5
+
+
+# ------------------------------------------- the torch CPU path (oracle/torch_ref.py)
+
+
+def test_torch_ref_to_mx_matches_golden_and_oracle():
+    """The torch restatement of to_mx (utils.py:84-105), which bench.py times on
+    the host's cores, gives the golden fixture's bytes and scales, and the
+    oracle's on special blocks (NaN, +-inf, zero, -0, denormal-only, saturating
+    448 / 464 / 480 * 2**k)."""
+    import os
+    from oracle import torch_ref as T
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1.npz"))
+    for name in ("a", "b"):
+        x = torch.from_numpy(z[name + "_bf16"].view(np.int16)).view(torch.bfloat16)
+        s, q = T.to_mx(x)
+        np.testing.assert_array_equal(s.numpy(), z[name + "_scales"])
+        np.testing.assert_array_equal(q.view(torch.uint8).numpy(), z[name + "_q"])
+    vals = [np.nan, -np.inf, np.inf, 0.0, -0.0, 2.0 ** -130, 448.0 * 2 ** 5, 464.0 * 2 ** -3, 480.0, 1.0, -3.5]
+    x = np.zeros((len(vals), 32), np.float32)
+    rng = np.random.default_rng(12)
+    for i, v in enumerate(vals):
+        x[i] = rng.standard_normal(32).astype(np.float32) * (0.0 if v == 0.0 or v == 2.0 ** -130 else 0.5)
+        x[i, 3] = v
+    s, q = T.to_mx(torch.from_numpy(x))
+    rs, rq = O.to_mx(x, src="f32")
+    np.testing.assert_array_equal(s.numpy(), rs)
+    np.testing.assert_array_equal(q.view(torch.uint8).numpy(), rq)
+
+
+def test_torch_ref_grouped_mm_matches_golden():
+    """Dequantize + one fp32 torch.matmul per group: within fp32 accumulation
+    error of the fp64 oracle on BASELINE config 1 (golden fixture), every
+    group (an empty one included) in place."""
+    import os
+    from oracle import torch_ref as T
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1.npz"))
+    t = lambda a, dt=torch.uint8: torch.from_numpy(np.ascontiguousarray(a)).view(dt)
+    out = T.grouped_mm(t(z["a_q"], torch.float8_e4m3fn), t(z["a_scales"]), t(z["b_q"], torch.float8_e4m3fn),
+                       t(z["b_scales"]), z["offs"])
+    ref = O.bf16_bits_to_f32(z["out_bf16"])
+    got = out.float().numpy()
+    assert O.rel_fro(ref, got) <= 4e-3          # bf16 rounding of both sides
+    assert np.mean(O.f32_to_bf16_bits(got) == z["out_bf16"]) > 0.99
+    # an empty group, rows past offs[-1] zero
+    offs = [0, 512, 512, 1000]
+    out = T.grouped_mm(t(z["a_q"], torch.float8_e4m3fn), t(z["a_scales"]), t(z["b_q"], torch.float8_e4m3fn),
+                       t(z["b_scales"]), offs).float().numpy()
+    ora = O.grouped_mm(z["a_q"], z["a_scales"], z["b_q"], z["b_scales"], offs)
+    assert O.rel_fro(ora[:1000], out[:1000]) <= 4e-3 and (out[1000:] == 0).all()
