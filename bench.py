@@ -710,6 +710,8 @@ def main():
                     help="time only the calls on step-major scales (the row-major kernel-only figures), not the "
                          "drop-in calls, which may stage operands in row pairs: for counter passes of the "
                          "row-major layout")
+    ap.add_argument("--ep-only", action="store_true",
+                    help="run only the expert-parallel shard measurement (E=1, M=2080; for kernel traces of it)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the BASELINE config 5 (e4m3 x e2m1) and quantizer measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -756,6 +758,9 @@ def main():
     offs_by_shape = {s: generate_jagged_offs(s[0], M_TOKENS, multiple_of=32, device=dev) for s in shapes}
     if args.copy_calibration:
         copy_calibration(dev)
+    if args.ep_only:
+        print(json.dumps({"ep_shard": ep_shard_measurement(dev, args, flush)}), flush=True)
+        return
 
     rows = []
     # per device kernel: summed event time (ms), FLOPs and launches of the timed reps

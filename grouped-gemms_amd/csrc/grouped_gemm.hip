@@ -1713,17 +1713,25 @@ struct TunedFwd {
 
 #include "tuned_fwd.h"
 
-// Tuned entry for (E, M, N, K, b_fmt) on operand layout `layout`: same E,
-// N, K and format, M within a factor of two of the swept M, and the operand
-// layout the sweep timed -- that of the drop-in call at the swept shape, with
-// its operands staged by the library's rule (dropin_layout) -- since the best
-// launch differs between layouts; null otherwise.
-const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int layout) {
+// Tuned entry for (E, M, N, K, b_fmt): same E, N, K and format, M within a
+// factor of two of the swept M; null when the sweep did not cover the shape.
+const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
   for (const TunedFwd* t = kTunedFwd; t->E; ++t)
-    if (t->E == E && t->N == N && t->K == K && t->b_fmt == b_fmt && 2 * M >= t->M && M <= 2 * (int64_t)t->M &&
-        layout == dropin_layout(t->E, t->M, t->N, t->K, t->b_fmt))
+    if (t->E == E && t->N == N && t->K == K && t->b_fmt == b_fmt && 2 * M >= t->M && M <= 2 * (int64_t)t->M)
       return t;
   return nullptr;
+}
+
+// Whether a tuned entry's tile order (GROUP_M, XCD swizzle) applies to a
+// call on operand layout `layout`: only on the layout the sweep timed --
+// that of the drop-in call at the swept shape, with its operands staged by
+// the library's rule (dropin_layout) -- since the best order differs between
+// layouts.  Its tile shape and split flag apply on every layout: the order
+// never changes the output bits, while the tile shape (through the split
+// plan) and the split can, and calls on different operand layouts give the
+// same bits.
+bool tuned_order_applies(const TunedFwd* t, int layout) {
+  return layout == dropin_layout(t->E, t->M, t->N, t->K, t->b_fmt);
 }
 
 // A tuned entry when the sweep covered the shape.  Otherwise 256 x 256
@@ -1742,8 +1750,13 @@ FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int layout
                    int xcd) {
   FwdChoice c{256, 256, 12, 8, true};
   const int64_t tiles256 = (cdiv(M, 256) + E - 1) * cdiv(N, 256);
-  if (const TunedFwd* t = find_tuned(E, M, N, K, b_fmt, layout)) {
-    c = FwdChoice{t->bm, t->bn, t->group_m, t->xcd, t->split != 0};
+  const TunedFwd* t = find_tuned(E, M, N, K, b_fmt);
+  if (t) {
+    c = FwdChoice{t->bm, t->bn, c.group_m, c.xcd, t->split != 0};
+    if (tuned_order_applies(t, layout)) {
+      c.group_m = t->group_m;
+      c.xcd = t->xcd;
+    }
   } else if (b_fmt == MXGG_FMT_E4M3 && tiles256 < 128) {
     // Under half a chip of 256 x 256 tiles: 128 x 128 tiles (two per CU)
     // spread the work over 4x the workgroups, unless the 256 x 256 launch
@@ -2367,6 +2380,32 @@ static int check_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, 
   return MXGG_OK;
 }
 
+// A wgrad launch whose 256 x 256 tiles would fill at most half the chip and
+// whose plan cuts none of them (a reduction too short to split, e.g. one GPU's
+// expert-parallel share, 2080 tokens, at N = K = 2048: 64 tiles on 256 CUs):
+// 128 x 128 tiles instead, four times as many, two workgroups per CU, whole.
+// p: the call's parameters with the 256 x 256 tile counts (replaced here).
+static int launch_wgrad_small(WgradParams p, bool al16, hipStream_t st) {
+  typedef CfgF8_128 Q;
+  p.tiles_n = (int)cdiv(p.N, Q::BM);
+  p.tiles_k = (int)cdiv(p.K, Q::BN);
+  p.part = nullptr;
+  p.dp = p.E * p.tiles_n * p.tiles_k;
+  p.S = 1;
+  p.units = 0;
+  p.dev = 0;
+  const dim3 grid((unsigned)(p.tiles_n * p.tiles_k), (unsigned)p.E);
+  if (p.out_dtype == MXGG_DTYPE_BF16 && al16)
+    hipLaunchKernelGGL((wgrad_kernel<Q, false, kEpiBf16>), grid, dim3(Q::NT), 0, st, p);
+  else if (p.out_dtype == MXGG_DTYPE_F16 && al16)
+    hipLaunchKernelGGL((wgrad_kernel<Q, false, kEpiF16>), grid, dim3(Q::NT), 0, st, p);
+  else if (p.out_dtype == MXGG_DTYPE_F16)
+    hipLaunchKernelGGL((wgrad_kernel<Q, false, kEpiF16Any>), grid, dim3(Q::NT), 0, st, p);
+  else
+    hipLaunchKernelGGL((wgrad_kernel<Q, false, kEpiAny>), grid, dim3(Q::NT), 0, st, p);
+  return launch_status("wgrad");
+}
+
 // The wgrad launches of a checked call on step-major scales (gs: GO [T][N],
 // is: IA [T][K] dwords); part / part_bytes: room for the fp32 partial tiles
 // of tiles cut along the tokens (none: no tile is cut).
@@ -2405,12 +2444,14 @@ static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, c
     p.par = par;
     p.slots = slots;
   }
+  const bool al16 = K % 8 == 0 && (uintptr_t)out % 16 == 0;
+  if (!p.dev && sp.units == 0 && 2 * tiles <= par)
+    return launch_wgrad_small(p, al16, st);
   const int64_t whole_ub = p.dev ? tiles : sp.dp;
   const int64_t units_ub = p.dev ? slots : sp.units;
   const int64_t split_tiles_ub = p.dev ? tiles : (sp.units ? sp.units / sp.S : 0);
   if (whole_ub > 0) {
     const dim3 grid((unsigned)(p.tiles_n * p.tiles_k), (unsigned)E);
-    const bool al16 = K % 8 == 0 && (uintptr_t)out % 16 == 0;
     if (out_dtype == MXGG_DTYPE_BF16 && al16)
       hipLaunchKernelGGL((wgrad_kernel<C, false, kEpiBf16>), grid, dim3(C::NT), 0, st, p);
     else if (out_dtype == MXGG_DTYPE_F16 && al16)

@@ -68,20 +68,37 @@ def _pair_buffer(batch: tuple, rows: int, length: int, device, group: int = 2) -
     Row pairs (``group`` 2, e4m3: ``MXGG_DATA_PAIRS``) and row quads (4,
     packed e2m1: ``MXGG_DATA_QUADS``), a layout with no counterpart in the
     reference: with pieces of ``P = 128 // group`` bytes (one 64-element
-    stage of a row) and ``ld = length`` rounded up to P, byte k of row r sits
+    stage of a row) and ``ld = _row_group_ld(length, P)`` (``length`` rounded
+    up to P, plus a pad at some lengths), byte k of row r sits
     at ``(r // group) * group * ld + (k // P) * 128 + (r % group) * P + k % P``,
     so the pieces of the rows of a group that the GEMMs stage together form
     one 128-byte line.  Returned as the strided view
-    ``(*batch, rows // group, group, ld // P, P)`` -- element ``[.., g, h, s, b]``
-    is byte ``P s + b`` of row ``group g + h`` -- so ``view.reshape(*batch,
-    rows, ld)`` gives the rows back (with the pad bytes past ``length``).
-    Returns ``(view, ld)``."""
+    ``(*batch, rows // group, group, cdiv(length, P), P)`` -- element
+    ``[.., g, h, s, b]`` is byte ``P s + b`` of row ``group g + h``, the group
+    stride ``group * ld`` -- so ``view.reshape(*batch, rows, -1)`` gives the
+    rows back (with the pad bytes past ``length`` up to the piece).  Returns
+    ``(view, ld)``."""
     if rows % group:
         raise ValueError(f"row {'pairs' if group == 2 else 'quads'} need a row count divisible by {group}, got {rows}")
     piece = 128 // group
-    ld = (length + piece - 1) // piece * piece
+    lv = (length + piece - 1) // piece * piece
+    ld = _row_group_ld(length, piece)
     buf = torch.empty(tuple(batch) + (rows // group, ld // piece, group, piece), dtype=torch.uint8, device=device)
-    return buf.transpose(-3, -2), ld
+    return buf[..., : lv // piece, :, :].transpose(-3, -2), ld
+
+
+def _row_group_ld(length: int, piece: int) -> int:
+    """Row stride of a row-group buffer for rows of ``length`` bytes: the
+    length rounded up to the piece, plus 192 bytes (never read) when the
+    rows span a multiple of 8 cache lines that is not a power of two (K =
+    3072, 5120, 6144, ...).  At those strides the 16 rows of a copy land on
+    few cache sets / channels: measured on MI355X, forward kernel-only time
+    on row pairs -2 to -7% at K = 5120 and dgrad at N = 5120 over the sweep
+    shapes (same bits); power-of-two line counts (2048, 4096, 8192) gain
+    nothing from it and keep the tight stride."""
+    ld = (length + piece - 1) // piece * piece
+    lines = (length + 127) // 128
+    return ld + 192 if lines % 8 == 0 and lines & (lines - 1) else ld
 
 
 def _pair_geometry(t: torch.Tensor, nbatch: int, group: int = 2):
@@ -102,13 +119,15 @@ def _pair_geometry(t: torch.Tensor, nbatch: int, group: int = 2):
 def _to_row_groups(q: torch.Tensor, group: int) -> torch.Tensor:
     *batch, R, L = q.shape
     batch = tuple(batch)
-    view, ld = _pair_buffer(batch, R, L, q.device, group)
+    view, _ = _pair_buffer(batch, R, L, q.device, group)
+    piece = 128 // group
+    lv = view.shape[-2] * piece            # the row's bytes rounded up to a piece
     src = q.view(torch.uint8)
-    if ld != L:
-        padded = torch.zeros(batch + (R, ld), dtype=torch.uint8, device=q.device)
+    if lv != L:
+        padded = torch.zeros(batch + (R, lv), dtype=torch.uint8, device=q.device)
         padded[..., :L] = src
         src = padded
-    view.copy_(src.reshape(batch + (R // group, group, ld // (128 // group), 128 // group)))
+    view.copy_(src.reshape(batch + (R // group, group, lv // piece, piece)))
     return view.view(q.dtype)
 
 

@@ -21,7 +21,9 @@ scales and skip their per-call re-layout.
 ``data_layout="pairs"`` makes them write the e4m3 data in row pairs: rows 2i
 and 2i+1 interleaved in 64-byte pieces, returned as the strided view
 ``(*batch, R/2, 2, cdiv(L, 64), 64)`` (``_common._pair_buffer``; the pad
-bytes past L are zero).  The GEMMs stage a 64-element slice of two adjacent
+bytes past L are zero; the pair stride grows by 192 unread bytes where the
+row spans a multiple of 8 cache lines that is not a power of two,
+``_common._row_group_ld``).  The GEMMs stage a 64-element slice of two adjacent
 rows per step, which is then one 128-byte line instead of halves of two:
 13% less time for the forward and 19% for the weight gradient over the
 benchmark shapes, same bits.  Packed e2m1 (32 bytes per 64-element step of a

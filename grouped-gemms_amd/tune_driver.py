@@ -122,10 +122,10 @@ def emit_header(best: dict, source: str = "", min_gain: float | None = None) -> 
         "// pick_fwd (grouped_gemm.hip) before its built-in rule.  Written by",
         "// `python grouped-gemms_amd/tune_driver.py --emit-header` from the sweep's",
         "// best.json; regenerate rather than edit.  An entry applies to calls with",
-        "// the same E, N, K and weight format, M within a factor of two of the swept",
-        "// M, and the operand layout the sweep timed: the drop-in call's, with the",
-        "// operands staged by the library's rule at the swept shape.  Fields: E, M, N,",
-        "// K, b_fmt (0 e4m3, 4 e2m1), block_m, block_n,",
+        "// the same E, N, K and weight format and M within a factor of two of the",
+        "// swept M; its GROUP_M and XCD swizzle only on the operand layout the sweep",
+        "// timed (the drop-in call's, operands staged by the library's rule at the",
+        "// swept shape).  Fields: E, M, N, K, b_fmt (0 e4m3, 4 e2m1), block_m, block_n,",
         "// group_m, xcd swizzle, split (1: the last round may be split along K when",
         "// the workspace allows it, 0: whole tiles only).",
         f"// sweep: {source or 'none'}",

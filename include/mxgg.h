@@ -195,8 +195,9 @@ int mxgg_tile_schedule(const int32_t* offs, int E, int64_t M, int64_t N, int blo
  * Replaces `_pick_config` / `_BEST_CFGS` / `_FALLBACK_*`
  * (kernels/forward.py:399-459).  The answer is the one for a
  * mxgg_grouped_mm call given room to stage its operands (the drop-in call):
- * tuned entries apply only to calls on the operand layout they were timed
- * on, so a *_steps call on another layout may get the built-in rule.
+ * a tuned entry's GROUP_M and XCD swizzle apply only to calls on the operand
+ * layout it was timed on, so a *_steps call on another layout may get the
+ * built-in order (tile shape and split stay the entry's: same bits).
  */
 int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int* block_m,
                            int* block_n, int* group_m, int* xcd_swizzle);

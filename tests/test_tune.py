@@ -120,10 +120,10 @@ def test_committed_table_is_used_by_the_library():
         # operand layout it was timed on: that of the drop-in call at the
         # swept shape, whose operand staging depends on M
         for m in (M, M // 2 + 1, 2 * M):
-            # (else the built-in rule: these swept shapes fill the chip with
-            # 256 x 256 tiles)
+            # (else the entry's tile with the built-in order: GROUP_M 12,
+            # 8-XCD swizzle)
             want = (bm, bn, gm, xcd) if _dropin_layout(lib, E, m, N, K, fmt) == \
-                _dropin_layout(lib, E, M, N, K, fmt) else (256, 256, 12, 8)
+                _dropin_layout(lib, E, M, N, K, fmt) else (bm, bn, 12, 8)
             assert _config(lib, E, m, N, K, fmt) == (0, want)
         # requests still override the table field by field
         assert _config(lib, E, M, N, K, fmt, (0, 0, 3, 1)) == (0, (bm, bn, 3, 1))
