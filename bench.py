@@ -312,6 +312,59 @@ def call_spans(trace_csv: str):
     return spans
 
 
+def ep_summary(trace_csv: str, ep_json: str) -> str:
+    """Per-call timeline of the expert-parallel shard measurement (``bench.py
+    --ep-only`` under ``rocprofv3 --kernel-trace``): its timed calls each follow
+    the 512 MB cache flush, so every run of kernels between two flushes is one
+    call.  The calls come in the measurement's order -- per (N, K): the drop-in
+    forward, the drop-in wgrad, then both on the native layout -- and each
+    (shape, kind) block is one run of consecutive calls with the same kernel
+    signature.  Per block: median span (first start to last end), and the
+    median duration of the scale re-layout launch and of each GEMM launch."""
+    import csv
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"].replace("void ", "").split("(")[0])
+                  for r in csv.DictReader(open(trace_csv)))
+    calls, cur = [], None
+    for t0, t1, n in rows:
+        if "FillFunctor" in n:
+            if cur:
+                calls.append(cur)
+            cur = []
+        elif cur is not None and n.startswith("mxgg::"):
+            cur.append((t0, t1, n))
+    if cur:
+        calls.append(cur)
+    short = lambda n: re.sub(r"mxgg::|\(.*", "", n)
+    blocks, sig = [], None
+    for c in calls:
+        if not c:
+            continue
+        g = tuple(short(n) for _, _, n in c)
+        if g != sig:
+            blocks.append([])
+            sig = g
+        blocks[-1].append(c)
+    ep = json.loads(open(ep_json).read().strip().splitlines()[-1])["ep_shard"]["rows"]
+    kinds = ("fwd drop-in", "wgrad drop-in", "fwd native", "wgrad native")
+    med = lambda xs: statistics.median(xs) if xs else 0.0
+    out = ["shape (N, K)   call            calls  span us  re-layout us  GEMM launches (median us each)"]
+    # the blocks of short warm-up runs (no flush in between) merge with a neighbour; keep those with most calls
+    blocks = [b for b in blocks if len(b) >= 10]
+    for i, b in enumerate(blocks):
+        shape = ep[i // 4] if i // 4 < len(ep) else {"N": "?", "K": "?"}
+        spans = [c[-1][1] - c[0][0] for c in b]
+        rl = [t1 - t0 for c in b for t0, t1, n in c if "relayout" in n]
+        gemm = {}
+        for c in b:
+            for t0, t1, n in c:
+                if "relayout" not in n:
+                    gemm.setdefault(short(n), []).append(t1 - t0)
+        g = "; ".join(f"{k} {med(v) / 1e3:.1f}" for k, v in gemm.items())
+        out.append(f"({shape['N']}, {shape['K']})  {kinds[i % 4]:14s} {len(b):6d} {med(spans) / 1e3:8.1f} "
+                   f"{med(rl) / 1e3 if rl else 0.0:12.1f}  {g}")
+    return "\n".join(out)
+
+
 def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str:
     """Per-kernel table of a ``rocprofv3 --kernel-trace --stats`` run over the
     default bench (its ``*_kernel_stats.csv``), the per-call GEMM spans from
@@ -720,6 +773,9 @@ def main():
                     help="summarize two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) of "
                          "`bench.py --steps S --warmup W --no-cpu --copy-calibration [--kernel-only]` (same S, W, "
                          "--shapes, --kernel-only) and exit; runs on the CPU")
+    ap.add_argument("--ep-summary", nargs=2, metavar=("TRACE_CSV", "EP_JSON"),
+                    help="per-call timeline of a rocprofv3 --kernel-trace run of `bench.py --ep-only` (its "
+                         "kernel_trace.csv and the JSON line it printed) and exit; runs on the CPU")
     ap.add_argument("--counter-summary", metavar="COUNTER_CSV",
                     help="per-kernel means of a rocprofv3 --pmc counter CSV and exit; runs on the CPU")
     ap.add_argument("--stats-summary", nargs="+", metavar="CSV",
@@ -729,6 +785,9 @@ def main():
     args = ap.parse_args()
     if args.counter_summary:
         print(counter_summary(args.counter_summary))
+        return
+    if args.ep_summary:
+        print(ep_summary(*args.ep_summary))
         return
     if args.stats_summary:
         print(stats_summary(*args.stats_summary))
