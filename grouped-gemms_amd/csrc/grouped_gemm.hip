@@ -1262,11 +1262,76 @@ struct ReduceShape {
   static_assert(NF % 4 == 0, "reduce items");
 };
 
+// Store one reduce item: fragments 4c .. 4c+3 of a tile, fragment f = 4c +
+// wave of the workgroup, with FN = 4 the column blocks j = 0 .. 3 of row
+// block i of wave tile wt, i.e. 32 rows x WTN columns.  16-bit outputs with
+// 16-byte aligned rows whose block lies wholly inside the tile go through LDS
+// (`blk`, 32 x WTN 16-bit values, 16-byte chunks XOR-swizzled by row), so
+// that each global store writes 4 whole row segments of WTN * 2 bytes; the
+// per-lane stores write 16 bytes of each of 32 rows instead.  Other outputs
+// take store_fragment_lane.  Every wave of the workgroup calls it for the
+// same item (the LDS path holds workgroup barriers; its condition is the
+// same for the four fragments).  Tiles of other wave shapes (FN != 4) take
+// the per-lane stores.
+template <class C, bool BF16_ONLY>
+__device__ __forceinline__ void store_item(const float (&v)[16], int f, int lane, uint8_t* out, int64_t ldo,
+                                           int rows, int cols, int out_dtype, uint8_t* blk) {
+  if constexpr (C::FN != 4) {
+    store_fragment_lane<C, BF16_ONLY>(v, f, lane, out, ldo, rows, cols, out_dtype);
+    return;
+  } else {
+  constexpr int RB = C::WTN * 2;                 // staged row bytes
+  constexpr int NCH = RB / 16;                   // 16-byte chunks per row
+  constexpr int RPI = 64 / NCH;                  // rows per store instruction
+  static_assert(NCH <= 64 && 64 % NCH == 0 && 32 % (4 * RPI) == 0, "reduce block shape");
+  const int wt = f / (C::FM * C::FN), i = (f / C::FN) % C::FM, j = f % C::FN;
+  const int r0 = (wt / C::WGN) * C::WTM + i * 32, c0 = (wt % C::WGN) * C::WTN;
+  const bool staged = out_dtype != MXGG_DTYPE_F32 && ldo % 8 == 0 && (uintptr_t)out % 16 == 0 &&
+                      r0 + 32 <= rows && c0 + C::WTN <= cols;
+  if (!staged) {
+    store_fragment_lane<C, BF16_ONLY>(v, f, lane, out, ldo, rows, cols, out_dtype);
+    return;
+  }
+  const int m = lane & 31, h = lane >> 5;
+  __syncthreads();                               // the previous item's reads of blk are done
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    uint32_t w0, w1;
+    if (out_dtype == MXGG_DTYPE_BF16) {
+      w0 = pack_bf16x2(v[4 * q4], v[4 * q4 + 1]);
+      w1 = pack_bf16x2(v[4 * q4 + 2], v[4 * q4 + 3]);
+    } else {
+      float f0 = v[4 * q4], f1 = v[4 * q4 + 1], f2 = v[4 * q4 + 2], f3 = v[4 * q4 + 3];
+      if (BF16_ONLY) {
+        f0 = round_bf16(f0); f1 = round_bf16(f1); f2 = round_bf16(f2); f3 = round_bf16(f3);
+      }
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      h2 x = {(_Float16)f0, (_Float16)f1}, y = {(_Float16)f2, (_Float16)f3};
+      w0 = __builtin_bit_cast(uint32_t, x);
+      w1 = __builtin_bit_cast(uint32_t, y);
+    }
+    const int c = 4 * j + q4;                    // 16-byte chunk (8 columns) of the block row
+    *reinterpret_cast<uint2*>(blk + m * RB + ((c ^ (m % NCH)) * 16) + 8 * h) = make_uint2(w0, w1);
+  }
+  __syncthreads();
+  const int wid = wave_id();
+#pragma unroll
+  for (int it = 0; it < 32 / (4 * RPI); ++it) {  // wave wid stores rows (32 / 4) wid ..
+    const int r = (wid * (32 / (4 * RPI)) + it) * RPI + lane / NCH;
+    const int c = lane % NCH;
+    const v4i val = *reinterpret_cast<const v4i*>(blk + r * RB + ((c ^ (r % NCH)) * 16));
+    __builtin_nontemporal_store(
+        val, reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(out) + (int64_t)(r0 + r) * ldo + c0 + c * 8));
+  }
+  }
+}
+
 // Split tiles of a forward launch: item (v, c) = fragments 4c .. 4c+3 of split
 // tile v, summed over its pieces and stored.  The plan is recomputed from
 // offs exactly as fwd_kernel computed it.
 template <class C>
 __global__ __launch_bounds__(256) void fwd_reduce_kernel(FwdParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t blk[32 * C::WTN * 2];
   WaveGroups wg;
   const int tiles = fwd_groups<C>(p, wg) * p.grid_n;
   const Split sp = fwd_split<C>(p, tiles);
@@ -1281,8 +1346,8 @@ __global__ __launch_bounds__(256) void fwd_reduce_kernel(FwdParams p) {
     if (!fwd_tile<C>(p, sp.dp + v, tiles, wg, tl)) continue;
     float acc[16];
     sum_pieces<C>(p.part + (int64_t)v * sp.S * (C::BM * C::BN), sp.S, f, lane, acc);
-    store_fragment_lane<C, false>(acc, f, lane, p.out + (tl.row0 * p.ldo + tl.n0) * esz, p.ldo, tl.rows,
-                                  tl.cols, p.out_dtype);
+    store_item<C, false>(acc, f, lane, p.out + (tl.row0 * p.ldo + tl.n0) * esz, p.ldo, tl.rows, tl.cols,
+                         p.out_dtype, blk);
   }
 }
 
@@ -1580,6 +1645,7 @@ __global__ __launch_bounds__(C::NT) void wgrad_kernel(WgradParams p) {
 // fwd_reduce_kernel; items past the plan's split tiles exit.
 template <class C>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t blk[32 * C::WTN * 2];
   constexpr int CH = ReduceShape<C>::CH;
   const int v = blockIdx.x / CH, f = (blockIdx.x % CH) * 4 + wave_id();
   int lt, base, S;
@@ -1589,8 +1655,8 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(WgradParams p) {
   float acc[16];
   sum_pieces<C>(p.part + (int64_t)base * (C::BM * C::BN), S, f, lane, acc);
   const int esz = p.out_dtype == MXGG_DTYPE_F32 ? 4 : 2;
-  store_fragment_lane<C, true>(acc, f, lane, p.out + ((int64_t)tl.g * p.N * p.K + tl.n0 * p.K + tl.k0) * esz,
-                               p.K, tl.rows, tl.cols, p.out_dtype);
+  store_item<C, true>(acc, f, lane, p.out + ((int64_t)tl.g * p.N * p.K + tl.n0 * p.K + tl.k0) * esz, p.K, tl.rows,
+                      tl.cols, p.out_dtype, blk);
 }
 
 // ---------------------------------------------------------------------------

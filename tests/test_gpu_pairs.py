@@ -369,6 +369,50 @@ def test_fwd_staged_activations_beside_e2m1_weight(gpu):
     assert torch.equal(ws[dst:dst + want.numel()], want)
 
 
+@pytest.mark.parametrize("L,ld", [(5120, 5120 + 192), (3072, 3072 + 192), (6144, 6144 + 192), (4096, 4096),
+                                  (8192, 8192), (2080, 2112)])
+def test_pair_stride_padded_at_bad_line_counts(gpu, L, ld):
+    """Row pairs of rows spanning a multiple of 8 cache lines that is not a
+    power of two get 192 unread bytes more per row in their stride
+    (_common._row_group_ld); the bytes sit at the documented offsets with
+    that ld, and the view still spans the row rounded up to 64."""
+    import kernels
+    from kernels._common import _pair_geometry
+    R = 4
+    x = _x((R, L), 7, gpu, 2.0)
+    _, q_r = kernels.to_mx(x)
+    _, q_p = kernels.to_mx(x, data_layout="pairs")
+    rows_, padded, got_ld = _pair_geometry(q_p, 0)
+    assert (rows_, padded, got_ld) == (R, (L + 63) // 64 * 64, ld)
+    flat = torch.as_strided(_u8(q_p), (R // 2 * 2 * ld,), (1,)).cpu().numpy()
+    r, k = np.meshgrid(np.arange(R), np.arange(L), indexing="ij")
+    at = (r // 2) * 2 * ld + (k // 64) * 128 + (r % 2) * 64 + k % 64
+    np.testing.assert_array_equal(flat[at], _u8(q_r).cpu().numpy())
+
+
+def test_drop_in_staging_opt_out(gpu, monkeypatch):
+    """MXGG_STAGING=0 drops the staging room from the drop-in calls' workspace
+    (forward and wgrad at staged benchmark shapes): the same bits."""
+    import random
+    import kernels
+    E, N, K = 1, 2048, 8192
+    offs = O.generate_jagged_offs(E, M_TOKENS, 32, rng=random.Random(4))
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    a = _x((M_TOKENS, K), 31, gpu)
+    w = _x((E, N, K), 32, gpu, 0.05)
+    sa, qa = kernels.to_mx(a)
+    sw, qw = kernels.to_mx(w)
+    sg, qg = kernels.to_mx_dim0(_x((M_TOKENS, N), 33, gpu))
+    si, qi = kernels.to_mx_dim0(a)
+    staged = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, o)
+    staged_w = kernels.triton_mxfp8_wgrad(qg, sg, qi, si, o)
+    monkeypatch.setenv("MXGG_STAGING", "0")
+    plain = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, o)
+    plain_w = kernels.triton_mxfp8_wgrad(qg, sg, qi, si, o)
+    assert torch.equal(staged.view(torch.uint8), plain.view(torch.uint8))
+    assert torch.equal(staged_w.view(torch.uint8), plain_w.view(torch.uint8))
+
+
 def test_fwd_drop_in_stages_the_weight(gpu):
     """The Python drop-in call on plain scales asks for the staging room
     (benchmark shape E=1, N=2048, K=8192): same bits as the step-scale call."""
