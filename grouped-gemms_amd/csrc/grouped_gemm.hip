@@ -1912,8 +1912,19 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   const int64_t tiles_ub = (int64_t)grid_m_ub * p.grid_n;
   if (tiles_ub <= 0) return MXGG_OK;
   if (tiles_ub > INT32_MAX) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: grid too large");
+  // The device's tile count is m * grid_n for some m <= grid_m_ub (each
+  // group adds whole m-blocks of grid_n tiles).  When every such count is
+  // below one round and its plan splits, no tile runs whole: the whole-tile
+  // launch would only route and exit (4.5 us on the expert-parallel shard's
+  // N = 2048, K = 8192 call), so it is left out.
+  bool whole = true;
+  if (p.slots && tiles_ub < p.par) {
+    whole = false;
+    for (int m = 1; m <= grid_m_ub && !whole; ++m)
+      if (split_plan(m * p.grid_n, p.par, nsteps, p.slots, C::BM * C::BN * 4 / 1024).units == 0) whole = true;
+  }
   const int epi = pick_epi(p.out_dtype, p.ldo, p.out);
-  switch (epi) {
+  if (whole) switch (epi) {
 #define MXGG_WHOLE(E) \
   case E: hipLaunchKernelGGL((fwd_kernel<C, false, E>), dim3((unsigned)tiles_ub), dim3(C::NT), 0, st, p); break
     MXGG_WHOLE(kEpiBf16);
