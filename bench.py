@@ -644,6 +644,45 @@ def extra_measurements(dev, args, flush):
     return {"cfg5": cfg5, "quant": quant, "moe_layer": moe, "ep_shard": ep}
 
 
+def round_sweep(dev, args, flush):
+    """Per-round time of whole forward launches against the reduction length:
+    E=1, M=16384, N=8192 is 2048 tiles of 256 x 256, exactly 8 rounds of the
+    256 resident workgroups (no split, no quarter-tile tail), at K = 256 ..
+    8192, on row-major data and on the native layout (step-major scales both).
+    A least-squares line over K >= 1024 (the ring runs at least 6 stages)
+    splits a round into a cost per 64-element stage and a fixed cost per tile
+    (set-up, the first copies' latency, the epilogue, the dispatch gap)."""
+    import torch
+    from kernels import to_mx, triton_mxfp8_grouped_mm
+    M, N, rounds = 16384, 8192, 8
+    offs = torch.tensor([M], dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    rows = []
+    for k in (256, 512, 1024, 2048, 4096, 8192):
+        a = torch.randn((M, k), device=dev, generator=g).to(torch.bfloat16)
+        w = (torch.randn((1, N, k), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        row = {"K": k, "stages": max(6, (k // 64 + 1) & ~1)}
+        for lay, kw in (("rows", {"scale_layout": "steps"}), ("pairs", {"scale_layout": "steps", "data_layout": "pairs"})):
+            sa, qa = to_mx(a, **kw)
+            sw, qw = to_mx(w, **kw)
+            med, _ = time_call(lambda: triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs), args.steps, args.warmup, flush)
+            row[f"{lay}_round_us"] = round(med * 1e3 / rounds, 2)
+            del sa, qa, sw, qw
+        rows.append(row)
+        del a, w
+    torch.cuda.empty_cache()
+    fit = {}
+    for lay in ("rows", "pairs"):
+        pts = [(r["stages"], r[f"{lay}_round_us"]) for r in rows if r["K"] >= 1024]
+        n = len(pts)
+        mx = sum(x for x, _ in pts) / n
+        my = sum(y for _, y in pts) / n
+        slope = sum((x - mx) * (y - my) for x, y in pts) / sum((x - mx) ** 2 for x, _ in pts)
+        fit[lay] = {"us_per_stage": round(slope, 3), "fixed_us_per_tile": round(my - slope * mx, 2)}
+    return {"workload": "E=1, M=16384, N=8192 forward (2048 tiles = 8 rounds of 256), step-major scales, "
+                        "cache-flushed calls", "rows": rows, "fit_K_ge_1024": fit}
+
+
 def ep_shard_measurement(dev, args, flush):
     """One GPU's share of the sweep under 8-way expert parallelism: E=8 over
     8 GPUs leaves one expert and about M/8 = 2080 tokens per GPU, so each
@@ -765,6 +804,8 @@ def main():
                          "row-major layout")
     ap.add_argument("--ep-only", action="store_true",
                     help="run only the expert-parallel shard measurement (E=1, M=2080; for kernel traces of it)")
+    ap.add_argument("--round-sweep", action="store_true",
+                    help="run only the per-round forward timing against K (per-stage and per-tile costs)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the BASELINE config 5 (e4m3 x e2m1) and quantizer measurements")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -819,6 +860,9 @@ def main():
         copy_calibration(dev)
     if args.ep_only:
         print(json.dumps({"ep_shard": ep_shard_measurement(dev, args, flush)}), flush=True)
+        return
+    if args.round_sweep:
+        print(json.dumps({"round_sweep": round_sweep(dev, args, flush)}), flush=True)
         return
 
     rows = []
