@@ -39,8 +39,8 @@ at full size with torch's intra-op threads, beside the GPU drop-in time of the
 same quantized operands.
 
 Prints ONE JSON line on stdout, with the per-shape medians of the sweep in its
-``rows`` field; progress and the per-shape table also go to stderr and to
-gpurun_out/bench_detail.json when that directory exists.
+``rows`` field; progress and the per-shape table also go to stderr and, when
+the output folder DETAIL_DIR (below) exists, to bench_detail.json there.
 """
 
 from __future__ import annotations
@@ -58,6 +58,7 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
+DETAIL_DIR = "gpurun_out"   # per-shape detail file goes here when the folder exists
 sys.path.insert(0, os.path.join(ROOT, "grouped-gemms_amd"))
 
 PEAK_MXFP8_TFLOPS = 5000.0          # MI355X published dense MXFP8 / FP8 peak
@@ -1047,7 +1048,7 @@ def main():
                           for r in rows]},
         "wall_s": round(time.time() - t_start, 1),
     }
-    outdir = os.path.join(ROOT, "gpurun_out")
+    outdir = os.path.join(ROOT, DETAIL_DIR)
     if os.path.isdir(outdir):
         with open(os.path.join(outdir, "bench_detail.json"), "w") as f:
             json.dump({"summary": line, "rows": rows}, f, indent=1)
