@@ -1266,24 +1266,20 @@ struct ReduceShape {
 // wave of the workgroup, with FN = 4 the column blocks j = 0 .. 3 of row
 // block i of wave tile wt, i.e. 32 rows x WTN columns.  16-bit outputs with
 // 16-byte aligned rows whose block lies wholly inside the tile go through LDS
-// (`blk`, 32 x WTN 16-bit values, 16-byte chunks XOR-swizzled by row), so
-// that each global store writes 4 whole row segments of WTN * 2 bytes; the
-// per-lane stores write 16 bytes of each of 32 rows instead.  Other outputs
-// take store_fragment_lane.  Every wave of the workgroup calls it for the
-// same item (the LDS path holds workgroup barriers; its condition is the
-// same for the four fragments).  Tiles of other wave shapes (FN != 4) take
-// the per-lane stores.
+// (store_item_lds), so that each global store writes 4 whole row segments of
+// WTN * 2 bytes; the per-lane stores (store_fragment_lane) write 16 bytes of
+// each of 32 rows instead, and serve every other output and tiles of other
+// wave shapes (FN != 4).  Every wave of the workgroup calls it for the same
+// item: the LDS path holds workgroup barriers, and its condition is the same
+// for the four fragments.
 template <class C, bool BF16_ONLY>
-__device__ __forceinline__ void store_item(const float (&v)[16], int f, int lane, uint8_t* out, int64_t ldo,
-                                           int rows, int cols, int out_dtype, uint8_t* blk) {
-  if constexpr (C::FN != 4) {
-    store_fragment_lane<C, BF16_ONLY>(v, f, lane, out, ldo, rows, cols, out_dtype);
-    return;
-  } else {
+__device__ __forceinline__ void store_item_lds(const float (&v)[16], int f, int lane, uint8_t* out, int64_t ldo,
+                                               int rows, int cols, int out_dtype, uint8_t* blk) {
   constexpr int RB = C::WTN * 2;                 // staged row bytes
-  constexpr int NCH = RB / 16;                   // 16-byte chunks per row
+  constexpr int NCH = RB / 16;                   // 16-byte chunks per row (XOR-swizzled by row in blk)
   constexpr int RPI = 64 / NCH;                  // rows per store instruction
-  static_assert(NCH <= 64 && 64 % NCH == 0 && 32 % (4 * RPI) == 0, "reduce block shape");
+  constexpr int RPW = 32 / C::NW;                // rows each wave stores
+  static_assert(NCH <= 64 && 64 % NCH == 0 && RPW % RPI == 0, "reduce block shape");
   const int wt = f / (C::FM * C::FN), i = (f / C::FN) % C::FM, j = f % C::FN;
   const int r0 = (wt / C::WGN) * C::WTM + i * 32, c0 = (wt % C::WGN) * C::WTN;
   const bool staged = out_dtype != MXGG_DTYPE_F32 && ldo % 8 == 0 && (uintptr_t)out % 16 == 0 &&
@@ -1316,14 +1312,22 @@ __device__ __forceinline__ void store_item(const float (&v)[16], int f, int lane
   __syncthreads();
   const int wid = wave_id();
 #pragma unroll
-  for (int it = 0; it < 32 / (4 * RPI); ++it) {  // wave wid stores rows (32 / 4) wid ..
-    const int r = (wid * (32 / (4 * RPI)) + it) * RPI + lane / NCH;
+  for (int it = 0; it < RPW / RPI; ++it) {       // wave wid: rows RPW wid .. RPW wid + RPW - 1
+    const int r = wid * RPW + it * RPI + lane / NCH;
     const int c = lane % NCH;
     const v4i val = *reinterpret_cast<const v4i*>(blk + r * RB + ((c ^ (r % NCH)) * 16));
     __builtin_nontemporal_store(
         val, reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(out) + (int64_t)(r0 + r) * ldo + c0 + c * 8));
   }
-  }
+}
+
+template <class C, bool BF16_ONLY>
+__device__ __forceinline__ void store_item(const float (&v)[16], int f, int lane, uint8_t* out, int64_t ldo,
+                                           int rows, int cols, int out_dtype, uint8_t* blk) {
+  if constexpr (C::FN == 4 && C::NW == 4)
+    store_item_lds<C, BF16_ONLY>(v, f, lane, out, ldo, rows, cols, out_dtype, blk);
+  else
+    store_fragment_lane<C, BF16_ONLY>(v, f, lane, out, ldo, rows, cols, out_dtype);
 }
 
 // Split tiles of a forward launch: item (v, c) = fragments 4c .. 4c+3 of split
