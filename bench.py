@@ -145,6 +145,28 @@ def read_trace_avg(kernel: str, native: bool):
     return None
 
 
+def read_dropin_gemm(kernel: str):
+    """The drop-in calls' figures of `kernel` in the committed kernel-trace
+    summary (profiles/kernel_stats_sweep.txt: the GEMM launches the sweep's
+    timed drop-in calls make, on operands staged in row pairs where the
+    library stages them, without and with their re-layout launch), or None."""
+    path = os.path.join(ROOT, "profiles", "kernel_stats_sweep.txt")
+    if not os.path.exists(path):
+        return None
+    pat = (r"the sweep's (\d+) drop-in calls of (.+?): GEMM launches ([\d.]+) us = ([\d.]+) TFLOP/s = ([\d.]+) of "
+           r".*re-layout launch \(([\d.]+) us\) ([\d.]+) TFLOP/s = ([\d.]+)")
+    for line in open(path):
+        m = re.search(pat, line)
+        if m and canon(m.group(2)) == canon(kernel):
+            return {"calls": int(m.group(1)), "gemm_us": float(m.group(3)), "achieved": float(m.group(4)),
+                    "frac": float(m.group(5)), "relayout_us": float(m.group(6)),
+                    "achieved_with_relayout": float(m.group(7)), "frac_with_relayout": float(m.group(8)),
+                    "source": "profiles/kernel_stats_sweep.txt: rocprofv3 kernel-trace spans of the GEMM launches "
+                              "inside the sweep's timed drop-in calls of a profiled run of this bench (operands as "
+                              "the drop-in call stages them), and of their re-layout launch"}
+    return None
+
+
 def copy_calibration(dev, mib: int = 256, reps: int = 3):
     """A plain device copy of known size, run so that a PMC pass over this
     program can scale FETCH_SIZE / WRITE_SIZE (the copy moves mib MiB each way)."""
@@ -313,6 +335,46 @@ def call_spans(trace_csv: str):
     return spans
 
 
+def dropin_spans(trace_csv: str):
+    """Drop-in calls in a ``rocprofv3 --kernel-trace`` CSV that directly
+    follow the bench's cache flush (its timed drop-in reps): the scale
+    re-layout launch (which also stages operands in row pairs where the
+    library does), then the call's GEMM dispatches.  Returns {whole-tile
+    kernel of the call: [(re-layout ns, GEMM span ns), ...]} in trace order;
+    a call whose every tile is split counts under the whole-tile kernel of its
+    configuration."""
+    import csv
+    rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"].replace("void ", "").split("(")[0])
+                  for r in csv.DictReader(open(trace_csv)))
+    out, i = {}, 0
+    while i + 1 < len(rows):
+        if "FillFunctor" in rows[i][2] and rows[i + 1][2].startswith("mxgg::scale_relayout_kernel"):
+            relayout = rows[i + 1][1] - rows[i + 1][0]
+            j, g0, g1, whole, piece, reduced = i + 2, None, None, None, None, False
+            while j < len(rows) and any(rows[j][2].startswith(g) for g in GEMM_KERNELS):
+                t0, t1, n = rows[j]
+                is_whole = ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n
+                is_piece = ", true, " in n and ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n)
+                # the next call's GEMM launches (unflushed warmup reps of the bench's next variant follow
+                # directly): a second whole-tile launch, or a piece launch after this call's reduce
+                if (is_whole and g0 is not None) or (is_piece and reduced):
+                    break
+                g0 = t0 if g0 is None else g0
+                g1 = t1 if g1 is None else max(g1, t1)
+                if is_whole:
+                    whole = n
+                elif is_piece:
+                    piece = piece or re.sub(r", true, \d+>$", ", false, 1>", n)
+                reduced = reduced or "_reduce_kernel<" in n
+                j += 1
+            if (whole or piece) and g0 is not None:
+                out.setdefault(whole or piece, []).append((relayout, g1 - g0))
+            i = j
+        else:
+            i += 1
+    return out
+
+
 def ep_summary(trace_csv: str, ep_json: str) -> str:
     """Per-call timeline of the expert-parallel shard measurement (``bench.py
     --ep-only`` under ``rocprofv3 --kernel-trace``): its timed calls each follow
@@ -403,6 +465,34 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
                 if nn and len(cold) >= nb + nn:
                     text += f";  the native sweep's {nn} after them: avg {sum(cold[nb:nb + nn]) / nn / 1e3:9.2f} us"
             out.append(text)
+    if trace_csv and line and line.get("roofline"):
+        # the GEMM launches the drop-in calls make, on the operands as the
+        # call hands them over (staged in row pairs where the library stages
+        # them); the sweep's timed drop-in reps are the first cold ones, and
+        # its forward + dgrad (wgrad) calls number what the kernel-only
+        # roofline counts, over the same shapes
+        rf = line["roofline"]
+        spans = dropin_spans(trace_csv)
+        out += ["", "Drop-in calls, from the same trace: each timed rep's scale re-layout launch (with any operand "
+                    "staging) and the span of its GEMM launches:"]
+        for name, v in sorted(spans.items()):
+            out.append(f"  {name:62s} calls {len(v):6d}: re-layout avg {sum(a for a, _ in v) / len(v) / 1e3:8.2f} us, "
+                       f"GEMM span avg {sum(b for _, b in v) / len(v) / 1e3:9.2f} us")
+        for key in (rf["kernel"], WGRAD_KERNEL):
+            v = spans.get(key) or spans.get(next((k for k in spans if canon(k) == canon(key)), ""), [])
+            bk = rf["by_kernel"].get(key)
+            if not bk or len(v) < bk["launches"]:
+                continue
+            nb = bk["launches"]
+            flops = bk["tflops"] * 1e12 * bk["avg_launch_us"] * 1e-6
+            gem = sum(b for _, b in v[:nb]) / nb
+            rel = sum(a for a, _ in v[:nb]) / nb
+            ach = flops / (gem * 1e-9) / 1e12
+            whole_call = flops / ((gem + rel) * 1e-9) / 1e12
+            out.append(f"  the sweep's {nb} drop-in calls of {key}: GEMM launches {gem / 1e3:.2f} us = {ach:.1f} "
+                       f"TFLOP/s = {ach / PEAK_MXFP8_TFLOPS:.3f} of {PEAK_MXFP8_TFLOPS} (dense MXFP8); with the "
+                       f"re-layout launch ({rel / 1e3:.2f} us) {whole_call:.1f} TFLOP/s = "
+                       f"{whole_call / PEAK_MXFP8_TFLOPS:.3f}")
     if line and line.get("roofline"):
         out += ["", "Same run, bench.py's own figures (HIP events on the launch stream, timed reps only):"]
         for key, tag in (("roofline", ""), ("roofline_native", NATIVE_TAG)):
@@ -534,6 +624,7 @@ def make_roofline(stats, tag, scope):
             "flops_per_launch": round(k["flops"] / k["launches"]),
             "launches": k["launches"],
             "profile": prof,
+            "dropin_gemm": None if tag else read_dropin_gemm(kname),
             "by_kernel": {n: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 2),
                               "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1),
                               "launches": v["launches"]} for n, v in stats.items()}}
