@@ -42,8 +42,7 @@ namespace mxgg {
 
 constexpr int BKS = 64;        // reduction elements per stage
 constexpr int STEP = 128;      // reduction elements per scale dword (4 blocks of 32)
-constexpr int SCG = 2;         // steps per scale group (one scale-ring slot)
-constexpr int SPG = SCG * STEP / BKS;   // stages per scale group
+constexpr int SCG = 2;         // steps per step-major scale group (one scale-ring slot)
 
 // Split of the last, partial round.  With T tiles and P workgroups resident
 // at once, the rem = T % P tiles of the last round leave most of the chip idle
@@ -130,7 +129,7 @@ __host__ __device__ inline void split_range(int a0, int n, int s, int S, int& a,
   b = a0 + (int)((uint32_t)n * (uint32_t)(s + 1) / (uint32_t)S);
 }
 
-template <int BM_, int BN_, int WGM_, int WGN_, int WFMT_, int NS_>
+template <int BM_, int BN_, int WGM_, int WGN_, int WFMT_, int NS_, bool PS_ = false>
 struct Cfg {
   static constexpr int BM = BM_;        // X rows per tile (output rows)
   static constexpr int BN = BN_;        // W rows per tile (output columns)
@@ -138,6 +137,11 @@ struct Cfg {
   static constexpr int WGN = WGN_;      // waves along columns
   static constexpr int WFMT = WFMT_;    // W element format (X is always e4m3)
   static constexpr int NS = NS_;        // ring depth (stages)
+  // Scale source: false, step-major dwords [step][row] (the re-layout
+  // kernel's output or the quantizer's native layout); true, the plain
+  // to_mx scales (row r's byte b at r * ld + b, ld a multiple of 16), read
+  // directly in 32-byte row pieces of 8 steps.
+  static constexpr bool PS = PS_;
   static constexpr bool F4 = WFMT == MXGG_FMT_E2M1;
   static constexpr int NW = WGM * WGN;
   static constexpr int NT = NW * kWave;
@@ -150,27 +154,40 @@ struct Cfg {
   static constexpr int XBYTES = BM * XROW;
   static constexpr int WBYTES = BN * WROW;
   static constexpr int STAGE = XBYTES + WBYTES;
-  // scale ring after the data ring: two slots, each SCG steps x BM X-row
-  // dwords ([step][row]) followed by SCG steps x BN W-row dwords
-  static constexpr int SSLOT = SCG * (BM + BN) * 4;
+  // scale ring after the data ring: two slots of GSTEPS steps each.
+  // Step-major: GSTEPS x BM X-row dwords ([step][row]) followed by GSTEPS x
+  // BN W-row dwords.  Plain: BM X rows then BN W rows of 32 bytes (steps
+  // 8c .. 8c+7 of the row, c = the group's chunk of the reduction), the two
+  // 16-byte halves of rows 8..15 of every 16 swapped (conflict-free reads of
+  // one step over 32 rows, two ways apart at most).
+  static constexpr int GSTEPS = PS ? 8 : SCG;           // steps per scale group (slot)
+  static constexpr int GSTAGES = GSTEPS * STEP / BKS;   // stages per scale group
+  static constexpr int SSLOT = GSTEPS * (BM + BN) * 4;
   static constexpr int SOFF = NS * STAGE;
   static constexpr int LDS = SOFF + 2 * SSLOT;
   static constexpr int QX = XBYTES / 1024 / NW;     // 1 KB data copies per wave and stage
   static constexpr int QW = WBYTES / 1024 / NW;
   static constexpr int LPS = QX + QW;               // LDS-DMA loads per wave and stage
-  static constexpr int NSX = SCG * BM * 4 / 1024;   // 1 KB scale copies of the X part (waves 0 ..)
-  static constexpr int NSD = SSLOT / 1024;          // 1 KB scale copies per group (X, then W)
+  // step-major: 1 KB scale copies of the X part (waves 0 ..) and per group
+  static constexpr int NSX = PS ? 0 : SCG * BM * 4 / 1024;
+  static constexpr int NSD = PS ? 0 : SSLOT / 1024;
+  // plain: 1 KB scale copies (32 rows) per wave and group; waves 0 .. NXW-1
+  // copy X rows, the others W rows
+  static constexpr int SPW = PS ? (BM + BN) / 32 / NW : 0;
+  static constexpr int NXW = PS ? BM / 32 / SPW : 0;
   static_assert(XBYTES % (1024 * NW) == 0 && WBYTES % (1024 * NW) == 0, "tile/wave split");
-  static_assert((SCG * BM * 4) % 1024 == 0 && (SCG * BN * 4) % 1024 == 0 && NSD <= NW,
+  static_assert(PS || ((SCG * BM * 4) % 1024 == 0 && (SCG * BN * 4) % 1024 == 0 && NSD <= NW),
                 "scale copies: one operand each, at most one per wave");
+  static_assert(!PS || (SPW >= 1 && (BM + BN) % (32 * NW) == 0 && (BM / 32) % SPW == 0),
+                "plain scale copies: whole 32-row pieces, one operand per wave");
   static_assert(BM % 4 == 0 && BN % 4 == 0, "scale pieces stay in one step");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   static_assert(NS >= 3 && LDS <= 160 * 1024, "ring depth / LDS budget");
-  // a scale group is copied SPG - 1 stages before its first read; the wait
-  // before that read covers it only if the stage read then was issued no
-  // earlier than the group
-  static_assert(NS <= SPG + 1, "ring deeper than the scale prefetch");
-  static_assert((NS - 1) * LPS <= 63, "vmcnt range");
+  // a scale group is copied GSTAGES - 1 stages (or more) before its first
+  // read; the wait before that read covers it only if the stage read then was
+  // issued no earlier than the group
+  static_assert(NS <= GSTAGES + 1, "ring deeper than the scale prefetch");
+  static_assert((NS - 1) * LPS + 2 * (PS ? SPW : 1) <= 63, "vmcnt range");
 };
 
 // 16-byte chunk swizzles: bijective on the chunk index for every 8-row and
@@ -229,7 +246,7 @@ __device__ __forceinline__ uint32_t operand_off(const Operand& O, uint32_t row, 
 // quantizer); reads past the buffer return 0.
 struct ScaleSrc {
   __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t rows;    // R: rows per step of that array
+  uint32_t rows;    // step-major: R, rows per step of that array; plain: bytes per row
   uint32_t row0;    // first row of the tile
 };
 
@@ -246,10 +263,14 @@ struct Frags {
 // (R rows: R * ld bytes in either layout, R being even) travels in the scalar
 // offset.  The chunk index rides in bits 28..31 (a lane's offset is at most
 // 31 rows, or 8 pairs, of a stride below 2**23 plus 112 bytes: below 2**28).
-// Scale copy of wave w (w < NSD): slot dwords 256 w .. 256 w + 255, 4 per
-// lane, of the X part (w < NSX) or the W part; lane l covers step u and tile
-// rows r .. r+3 of its operand, at byte s_base + t * s_step of that
-// operand's scale buffer for step t of the reduction.
+// Scale copy of wave w, step-major (w < NSD): slot dwords 256 w .. 256 w +
+// 255, 4 per lane, of the X part (w < NSX) or the W part; lane l covers step
+// u and tile rows r .. r+3 of its operand, at byte s_base + t * s_step of that
+// operand's scale buffer for step t of the reduction.  Plain: copy i of wave
+// w fills slot rows 32 (w SPW + i) .. +31 (X rows for w < NXW, then W rows);
+// lane l holds 16 bytes of row l / 2 of the copy, the half (l ^ (l >> 4)) & 1
+// of the row's 32-byte piece, at byte s_base + i * s_step + 4 t of that
+// operand's scales for the piece starting at step t.
 template <class C>
 struct Plan {
   uint32_t xoff;
@@ -277,14 +298,23 @@ __device__ __forceinline__ void make_plan(Plan<C>& P, const Operand& X, const Op
     P.woff = operand_off(W, (uint32_t)row, (uint32_t)c * 16u) | ((uint32_t)c << 28);
   }
   const int wave = wave_id();
-  const bool isx = wave < C::NSX;
-  const int R = isx ? C::BM : C::BN;              // tile rows of the lane's operand
-  const int q = (isx ? wave : wave - C::NSX) * 256 + 4 * lane;   // first dword of the lane in its part
-  const int u = q / R;                            // step of the group
-  const ScaleSrc& S = isx ? xs : ws;
-  const uint32_t r = S.row0 + (uint32_t)(q % R);
-  P.s_step = S.rows * 4u;
-  P.s_base = r * 4u + (uint32_t)u * P.s_step;
+  if constexpr (C::PS) {
+    const bool isx = wave < C::NXW;
+    const ScaleSrc& S = isx ? xs : ws;
+    const int row = (isx ? wave : wave - C::NXW) * C::SPW * 32 + lane / 2;   // operand row of the tile
+    const int h = (lane ^ (lane >> 4)) & 1;
+    P.s_step = S.rows * 32u;
+    P.s_base = (S.row0 + (uint32_t)row) * S.rows + (uint32_t)h * 16u;
+  } else {
+    const bool isx = wave < C::NSX;
+    const int R = isx ? C::BM : C::BN;              // tile rows of the lane's operand
+    const int q = (isx ? wave : wave - C::NSX) * 256 + 4 * lane;   // first dword of the lane in its part
+    const int u = q / R;                            // step of the group
+    const ScaleSrc& S = isx ? xs : ws;
+    const uint32_t r = S.row0 + (uint32_t)(q % R);
+    P.s_step = S.rows * 4u;
+    P.s_base = r * 4u + (uint32_t)u * P.s_step;
+  }
 }
 
 // Global -> LDS copies of stage `st` (elements [64 st, 64 st + 64)) into slot
@@ -343,18 +373,58 @@ __device__ __forceinline__ void dma16_if(int go, __amdgpu_buffer_rsrc_t rsrc, ui
 #endif
 }
 
+// dma16_if with a scalar byte offset `soff` added to the address.
+__device__ __forceinline__ void dma16_if_so(int go, __amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff,
+                                            uint32_t lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t saved;
+  asm volatile(
+      "s_cmp_eq_u32 %1, 0\n\t"
+      "s_cbranch_scc1 1f\n\t"
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %4, %5 offen lds\n\t"
+      "s_mov_b32 m0, %0\n"
+      "1:"
+      : "=&s"(saved)
+      : "s"(go), "v"(voff), "s"(lds), "s"(rsrc), "s"(soff)
+      : "memory", "scc");
+#endif
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr_t)(const_cast<void*>(p));
 }
 
-// Scale group g (steps tg .. tg+SCG-1) into scale slot `ss` (waves w < NSD
-// copy 1 KB each; ssr: the scale buffer of the wave's operand).
+// Scale group of steps tg .. tg+GSTEPS-1 into scale slot `ss` (ssr: the
+// scale buffer of the wave's operand).  Step-major: waves w < NSD copy 1 KB
+// each; plain: every wave copies SPW pieces of 32 rows (tg a multiple of 8).
 template <class C>
 __device__ __forceinline__ void issue_scales(uint8_t* ss, __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P,
                                              int tg, bool live) {
   const int wave = wave_id();
-  const int go = (live && wave < C::NSD) ? 1 : 0;
-  dma16_if(uniform(go), ssr, P.s_base + (uint32_t)tg * P.s_step, lds_addr(ss + wave * 1024));
+  if constexpr (C::PS) {
+    const int go = uniform(live ? 1 : 0);
+    const uint32_t v = P.s_base + (uint32_t)tg * 4u;
+#pragma unroll
+    for (int i = 0; i < C::SPW; ++i)
+      dma16_if_so(go, ssr, v, (uint32_t)uniform((int)(P.s_step * (uint32_t)i)), lds_addr(ss + (wave * C::SPW + i) * 1024));
+  } else {
+    const int go = (live && wave < C::NSD) ? 1 : 0;
+    dma16_if(uniform(go), ssr, P.s_base + (uint32_t)tg * P.s_step, lds_addr(ss + wave * 1024));
+  }
+}
+
+// Plain scales: piece i (rows 32 (w SPW + i) .. +31 of the slot) of the group
+// of steps tg .. tg+7 into scale slot `ss`, when `live` (wave-uniform i).
+template <class C>
+__device__ __forceinline__ void issue_scale_piece(uint8_t* ss, __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P,
+                                                  int tg, int i, bool live) {
+  static_assert(C::PS, "plain scales");
+  const int wave = wave_id();
+  dma16_if_so(uniform(live ? 1 : 0), ssr, P.s_base + (uint32_t)tg * 4u, (uint32_t)uniform((int)(P.s_step * (uint32_t)i)),
+              lds_addr(ss + (wave * C::SPW + i) * 1024));
 }
 
 // Fragments and raw scale dwords of the stage in data slot `sb`, whose step is
@@ -391,12 +461,22 @@ __device__ __forceinline__ void read_stage(const uint8_t* sb, const uint8_t* ss,
       F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
-  const uint32_t* sx = reinterpret_cast<const uint32_t*>(ss) + u * C::BM;
-  const uint32_t* sy = reinterpret_cast<const uint32_t*>(ss) + SCG * C::BM + u * C::BN;
+  if constexpr (C::PS) {
+    // slot row m: 8 dwords, half (u / 4) ^ ((m >> 3) & 1) holding steps 4 (u / 4) ..
+    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(ss);
+    const int d = ((((u >> 2) ^ (r32 >> 3)) & 1) << 2) | (u & 3);
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i) xs[i] = sx[wm * C::WTM + i * 32 + r32];
+    for (int i = 0; i < C::FM; ++i) xs[i] = s32[(wm * C::WTM + i * 32 + r32) * 8 + d];
 #pragma unroll
-  for (int j = 0; j < C::FN; ++j) ws[j] = sy[wn * C::WTN + j * 32 + r32];
+    for (int j = 0; j < C::FN; ++j) ws[j] = s32[(C::BM + wn * C::WTN + j * 32 + r32) * 8 + d];
+  } else {
+    const uint32_t* sx = reinterpret_cast<const uint32_t*>(ss) + u * C::BM;
+    const uint32_t* sy = reinterpret_cast<const uint32_t*>(ss) + C::GSTEPS * C::BM + u * C::BN;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) xs[i] = sx[wm * C::WTM + i * 32 + r32];
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) ws[j] = sy[wn * C::WTN + j * 32 + r32];
+  }
 }
 
 // Move the scale byte of the lane's 32-element block of stage st (block
@@ -492,7 +572,12 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   const int rn = r + 1;
   uint8_t* cur = smem + (r % C::NS) * C::STAGE;
   const uint8_t* nxt = smem + (rn % C::NS) * C::STAGE;
-  const uint8_t* snx = smem + C::SOFF + ((rn / SPG) & 1) * C::SSLOT;
+  // scale groups: GSTAGES stages each, counted from the ring's first stage
+  // (step-major) or from the 8-step piece holding it (plain: g0 stages into
+  // it; its first step tb a multiple of 8)
+  const int g0 = C::PS ? (s0 & (C::GSTAGES - 1)) : 0;
+  const int gr = g0 + rn;
+  const uint8_t* snx = smem + C::SOFF + ((gr / C::GSTAGES) & 1) * C::SSLOT;
   if constexpr (TAIL == kStageLast) {
     mfma_range<C, 0, NMMA, FIRST>(Fc, xc, wc, acc);
     hold(Fc, xc, wc);
@@ -514,15 +599,25 @@ __device__ __forceinline__ void ring_stage(uint8_t* smem, const Operand& X, cons
   // LDS reads first, then the copies: a read issued after an LDS-DMA load
   // may otherwise be given the load's offset register as its destination
   // while the load still uses it.
-  read_stage<C>(nxt, snx, (rn / 2) % SCG, Fn, xn, wn);
-  // stage r+1 opening scale group g = (r+1)/SPG frees the slot of group g-1
+  read_stage<C>(nxt, snx, (gr / 2) % C::GSTEPS, Fn, xn, wn);
+  // stage r+1 opening scale group g = gr / GSTAGES frees the slot of group g-1
   // (last read, of stage r, before this barrier): group g+1 goes there
   // (a group that starts past the reduction range is never read: not copied,
   // so the drain after the last stage waits for no memory read)
   if constexpr (TAIL == kStageFull) {
-    const int tg = s0 / 2 + (rn / SPG + 1) * SCG;
-    const bool opens = rn % SPG == 0 && tg * STEP < hi;
-    issue_scales<C>(smem + C::SOFF + ((rn / SPG + 1) & 1) * C::SSLOT, ssr, P, tg, opens);
+    const int tg = (s0 - g0) / 2 + (gr / C::GSTAGES + 1) * C::GSTEPS;
+    uint8_t* sn = smem + C::SOFF + ((gr / C::GSTAGES + 1) & 1) * C::SSLOT;
+    if constexpr (C::PS) {
+      // plain: the group's SPW pieces one per stage over its first SPW
+      // stages (a burst of copies stalls the waves' issue); a group whose
+      // later pieces would fall on the copy-free last stages starts at or
+      // past the last stage, so it is never read (and tg * STEP >= hi)
+      const int gs = gr % C::GSTAGES;
+      issue_scale_piece<C>(sn, ssr, P, tg, gs < C::SPW ? gs : 0, gs < C::SPW && tg * STEP < hi);
+    } else {
+      const bool opens = gr % C::GSTAGES == 0 && tg * STEP < hi;
+      issue_scales<C>(sn, ssr, P, tg, opens);
+    }
     issue_stage<C>(cur, X, W, P, s0 + r + C::NS, lo, hi);
   }
   mfma_range<C, NE, NMMA, FIRST>(Fc, xc, wc, acc);
@@ -563,18 +658,20 @@ __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, c
   Plan<C> P;
   make_plan<C>(P, X, W, xss, wss);
   // the scale buffer this wave copies from (wave-uniform)
-  const __amdgpu_buffer_rsrc_t ssr = wave_id() < C::NSX ? xss.rsrc : wss.rsrc;
+  const __amdgpu_buffer_rsrc_t ssr = wave_id() < (C::PS ? C::NXW : C::NSX) ? xss.rsrc : wss.rsrc;
   // scale groups 0 and 1, then stages s0 .. s0+NS-1 (scales first: every
   // wait for a stage's copies then covers the scale copies issued before it)
-  issue_scales<C>(smem + C::SOFF, ssr, P, s0 / 2, true);
-  issue_scales<C>(smem + C::SOFF + C::SSLOT, ssr, P, s0 / 2 + SCG, true);
+  const int g0 = C::PS ? (s0 & (C::GSTAGES - 1)) : 0;
+  const int tb = (s0 - g0) / 2;
+  issue_scales<C>(smem + C::SOFF, ssr, P, tb, true);
+  issue_scales<C>(smem + C::SOFF + C::SSLOT, ssr, P, tb + C::GSTEPS, true);
 #pragma unroll
   for (int i = 0; i < C::NS; ++i) issue_stage<C>(smem + i * C::STAGE, X, W, P, s0 + i, lo, hi);
   MXGG_WAIT_VM((C::NS - 1) * C::LPS);
   MXGG_BARRIER();
   Frags<C> Fa, Fb;
   uint32_t xa[C::FM], wa[C::FN], xb[C::FM], wb[C::FN];
-  read_stage<C>(smem, smem + C::SOFF, 0, Fa, xa, wa);
+  read_stage<C>(smem, smem + C::SOFF, g0 / 2, Fa, xa, wa);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   finish_scales<C>(xa, wa, s0, lo, hi);
   const int n = s1 - s0;
@@ -620,7 +717,7 @@ template <class C>
 __device__ __forceinline__ void edge_chunk(const Operand& X, const Operand& W, const ScaleSrc& xss,
                                            const ScaleSrc& wss, int cs, int lo, int hi,
                                            v16f (&acc)[C::FM][C::FN]) {
-  static_assert(!C::F4, "edge chunks: e4m3 operands only");
+  static_assert(!C::F4 && !C::PS, "edge chunks: e4m3 operands, step-major scales only");
   const int wave = wave_id();
   const int lane = threadIdx.x % kWave;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
@@ -1032,14 +1129,19 @@ __global__ __launch_bounds__(256) void scale_relayout_kernel(ScaleJobs js) {
 struct FwdParams {
   const uint8_t* a; int64_t lda;
   const uint8_t* b; int64_t ldb_n; int64_t ldb_e;
-  const uint8_t* as; uint32_t as_bytes;     // A scales, step-major [T][M] dwords (T = cdiv(K, 128))
-  const uint8_t* bs; uint32_t bs_expert;    // B scales, step-major [E][T][N] dwords; bytes per expert
+  // A scales: step-major [T][M] dwords (T = cdiv(K, 128)), or (plain-scale
+  // kernels, Cfg::PS) to_mx's (M, K/32) bytes with row stride as_ld; B
+  // scales: step-major [E][T][N] dwords, or plain (E, N, K/32) with row
+  // stride bs_ld.  as_bytes / bs_expert: bytes of A's / of one expert's scales.
+  const uint8_t* as; uint32_t as_bytes;
+  const uint8_t* bs; uint32_t bs_expert;
   const int32_t* offs; int E; int64_t M; int64_t N; int64_t K;
   uint8_t* out; int out_dtype; int64_t ldo;
   int grid_n; int group_m; int xcd;
   float* part; int par; int slots;          // split: partial slots, resident workgroups, slot count
   int quads;                                // last round as 128 x 128 quarter tiles (quad_dp)
   int a_pl; int b_pl;                       // operand layouts: 0 rows, 1 row pairs, 2 row quads (Operand)
+  uint32_t as_ld; uint32_t bs_ld;           // plain scales: bytes per row (multiples of 16)
 };
 
 // Epilogue of the whole-tile kernels, fixed at compile time so that the
@@ -1119,8 +1221,9 @@ __device__ __forceinline__ void fwd_tile_run(const FwdParams& p, uint8_t* smem, 
 
   const Operand X = make_operand(p.a, p.lda, p.a_pl, row0, rows);
   const Operand W = make_operand(p.b + (int64_t)tl.expert * p.ldb_e, p.ldb_n, p.b_pl, n0, cols);
-  const ScaleSrc xs{make_rsrc(p.as, p.as_bytes), (uint32_t)p.M, (uint32_t)row0};
-  const ScaleSrc ws{make_rsrc(p.bs + (int64_t)tl.expert * p.bs_expert, p.bs_expert), (uint32_t)p.N, (uint32_t)n0};
+  const ScaleSrc xs{make_rsrc(p.as, p.as_bytes), C::PS ? p.as_ld : (uint32_t)p.M, (uint32_t)row0};
+  const ScaleSrc ws{make_rsrc(p.bs + (int64_t)tl.expert * p.bs_expert, p.bs_expert), C::PS ? p.bs_ld : (uint32_t)p.N,
+                    (uint32_t)n0};
 
   v16f acc[C::FM][C::FN];   // set by ring_mainloop
   const int K = (int)p.K;
@@ -1769,6 +1872,17 @@ typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_128;
 // measured the same on BASELINE config 5, 650 vs 651 us, and spilled 8 bytes
 // per lane in the LDS-staged epilogues)
 typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 4> CfgF4_256;
+// The same tiles on plain to_mx scales (drop-in calls whose scale rows are
+// 16-byte multiples): no scale re-layout launch; 16 KB scale slots of 8 steps
+// (8 KB for 128 x 128 tiles).
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 4, true> CfgF8_256P;
+typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3, 4, true> CfgF8_128P;
+typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 4, true> CfgF4_256P;
+
+// The scale-independent kernels of a configuration (the reduce): its
+// step-major twin.
+template <class C>
+using StepCfg = Cfg<C::BM, C::BN, C::WGM, C::WGN, C::WFMT, C::NS>;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -1907,7 +2021,9 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   // quarter tiles (quad_dp).  The device decides from the real tile count;
   // the host, from the usual one, only skips the launch where it cannot help.
   p.quads = 0;
-  if constexpr (std::is_same<C, CfgF8_256>::value) {
+  constexpr bool kQuads = std::is_same<C, CfgF8_256>::value || std::is_same<C, CfgF8_256P>::value;
+  typedef typename std::conditional<C::PS, CfgF8_128P, CfgF8_128>::type Q;
+  if constexpr (kQuads) {
     if (nsteps < kMinSplitTotal && p.par > 0) {
       const int64_t est = (cdiv(p.M, C::BM) + (p.E - 1) / 2) * p.grid_n;
       if (est <= INT32_MAX && quad_dp((int)est, p.par) < est) p.quads = 1;
@@ -1939,12 +2055,12 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
 #undef MXGG_WHOLE
   }
   if (int rc = launch_status("grouped_mm")) return rc;
-  if constexpr (std::is_same<C, CfgF8_256>::value) {
+  if constexpr (kQuads) {
     if (p.quads) {   // 4 * (T % P) <= P quarters
       switch (epi) {
 #define MXGG_QUAD(E)                                                                                         \
   case E:                                                                                                   \
-    hipLaunchKernelGGL((fwd_quad_kernel<C, CfgF8_128, E>), dim3((unsigned)p.par), dim3(CfgF8_128::NT), 0, st, p); \
+    hipLaunchKernelGGL((fwd_quad_kernel<C, Q, E>), dim3((unsigned)p.par), dim3(Q::NT), 0, st, p); \
     break
         MXGG_QUAD(kEpiBf16);
         MXGG_QUAD(kEpiF16);
@@ -1972,7 +2088,7 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   if (rgrid < 128) rgrid = 128;
   if (rgrid > items) rgrid = items;
   if (rgrid <= 0) return MXGG_OK;
-  hipLaunchKernelGGL((fwd_reduce_kernel<C>), dim3((unsigned)rgrid), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((fwd_reduce_kernel<StepCfg<C>>), dim3((unsigned)rgrid), dim3(256), 0, st, p);
   return launch_status("grouped_mm");
 }
 
@@ -2204,13 +2320,27 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
   return MXGG_OK;
 }
 
+// Plain to_mx scales the GEMMs can read directly (plain-scale kernels): rows
+// of 16-byte multiples, 16-byte aligned buffers, byte ranges below 2**31.
+constexpr int64_t kPlainMaxMacs = (int64_t)60000000000;   // 1.2e11 flop
+
+static bool plain_scales_ok(const uint8_t* A_s, int64_t ldas, const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
+                            int E, int64_t M, int64_t N) {
+  if (ldas % 16 || ldbs_n % 16 || (E > 1 && ldbs_e % 16) || !aligned16(A_s) || !aligned16(B_s)) return false;
+  const int64_t bexp = E > 1 ? ldbs_e : N * ldbs_n;
+  return M * ldas < ((int64_t)1 << 31) && bexp < ((int64_t)1 << 31) && (int64_t)(E - 1) * bexp < ((int64_t)1 << 40);
+}
+
 // The GEMM launches of a checked forward call on step-major scales (as: A
-// [T][M], bs: B [E][T][N] dwords); part / part_bytes: room for the fp32
+// [T][M], bs: B [E][T][N] dwords), or, with `plain`, on plain to_mx scales
+// (as: A (M, K/32) with row stride ldas, bs: B (E, N, K/32) with strides
+// ldbs_n, ldbs_e; plain_scales_ok holds); part / part_bytes: room for the fp32
 // partial tiles of a split last round (none: no tile is split).
 static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, const uint8_t* B, int b_fmt,
                              int64_t ldb_n, int64_t ldb_e, const uint8_t* bs, const int32_t* offs, int E, int64_t M,
                              int64_t N, int64_t K, void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
-                             int group_m, int xcd, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
+                             int group_m, int xcd, int layout, void* part_area, size_t part_bytes, hipStream_t st,
+                             bool plain = false, int64_t ldas = 0, int64_t ldbs_n = 0, int64_t ldbs_e = 0) {
   FwdChoice c = pick_fwd(E, M, N, K, b_fmt, layout, block_m, block_n, group_m, xcd);
   const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
                                            : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
@@ -2225,16 +2355,25 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
   const size_t pb = part ? (part_bytes < cap ? part_bytes : cap) : 0;
   if (!pb) part = nullptr;
   p.part = part;
-  if (b_fmt == MXGG_FMT_E2M1)
-    return launch_fwd<CfgF4_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
-  if (c.bm == 256)
-    return launch_fwd<CfgF8_256>(p, (int)(cdiv(M, 256) + E - 1), c.group_m, c.xcd, pb, st);
-  return launch_fwd<CfgF8_128>(p, (int)(cdiv(M, 128) + E - 1), c.group_m, c.xcd, pb, st);
+  const int gm256 = (int)(cdiv(M, 256) + E - 1), gm128 = (int)(cdiv(M, 128) + E - 1);
+  if (plain) {
+    p.as_bytes = (uint32_t)(M * ldas);
+    p.bs_expert = (uint32_t)(E > 1 ? ldbs_e : N * ldbs_n);
+    p.as_ld = (uint32_t)ldas;
+    p.bs_ld = (uint32_t)ldbs_n;
+    if (b_fmt == MXGG_FMT_E2M1) return launch_fwd<CfgF4_256P>(p, gm256, c.group_m, c.xcd, pb, st);
+    if (c.bm == 256) return launch_fwd<CfgF8_256P>(p, gm256, c.group_m, c.xcd, pb, st);
+    return launch_fwd<CfgF8_128P>(p, gm128, c.group_m, c.xcd, pb, st);
+  }
+  if (b_fmt == MXGG_FMT_E2M1) return launch_fwd<CfgF4_256>(p, gm256, c.group_m, c.xcd, pb, st);
+  if (c.bm == 256) return launch_fwd<CfgF8_256>(p, gm256, c.group_m, c.xcd, pb, st);
+  return launch_fwd<CfgF8_128>(p, gm128, c.group_m, c.xcd, pb, st);
 }
 
-// A checked forward call on plain scales: re-lay them step-major into the
-// workspace, then the GEMM launches (partial tiles after the scales, when
-// there is room).
+// A checked forward call on plain scales: the GEMM launches, on the plain
+// scales where plain_scales_ok holds, else after re-laying them step-major
+// into the workspace (the partial tiles follow the room of those scales in
+// either case, so both ways make the same split plan and the same bits).
 static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas, const uint8_t* B,
                           int b_fmt, int64_t ldb_n, int64_t ldb_e, const uint8_t* B_s, int64_t ldbs_n,
                           int64_t ldbs_e, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
@@ -2258,18 +2397,30 @@ static int run_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int
   const bool staged_a = T > 0 && stage_a && wl.extra >= used_b + stage_a;
   if (staged_a)
     pa = PairJob{A, lda, 0, (uint8_t*)align256((size_t)(end - used_b - stage_a)), ldp, (int)(M / 2), 1, (int)K};
-  if (T > 0) {
+  // The plain-scale kernels save the scale re-layout launch (4.4 us at the
+  // least, a quarter of the smallest expert-parallel shard call) but copy
+  // their scales in 32-byte row pieces, four times the copy requests of the
+  // step-major dwords, which slows the main loop by about 3%.  Measured on
+  // MI355X (drop-in forward, same bits either way): E = 1, M = 2080 calls of
+  // 1.7e10 .. 1.1e11 flop -13 to -1.5%, 1.7e11 +0.6 to +2.6%, and the
+  // 36-shape sweep (1.4e11 flop and up) +2.7% geomean.  So they run on calls
+  // that stage nothing (staging launches the re-layout kernel anyway) of at
+  // most kPlainMaxMacs multiply-adds.
+  const bool plain = !staged_a && !staged_b && M * N <= kPlainMaxMacs / (K > 0 ? K : 1) &&
+                     plain_scales_ok(A_s, ldas, B_s, ldbs_n, ldbs_e, E, M, N);
+  if (T > 0 && !plain) {
     if (int rc = launch_relayout(scale_job(A_s, ldas, 0, wsd, M, 1, K / 32, T),
                                  scale_job(B_s, ldbs_n, ldbs_e, wsd + T * M, N, E, K / 32, T), st, "grouped_mm",
                                  staged_b ? &pb : nullptr, staged_a ? &pa : nullptr))
       return rc;
   }
   void* part = wl.part ? (void*)((uint8_t*)workspace + wl.part_off) : nullptr;
-  return launch_grouped_mm(staged_a ? pa.dst : A, staged_a ? (int64_t)ldp : lda, (const uint8_t*)wsd,
-                           staged_b ? pb.dst : B, b_fmt, staged_b ? (int64_t)ldp : ldb_n,
-                           staged_b ? N * ldp : ldb_e, (const uint8_t*)(wsd + T * M), offs, E, M, N, K, out,
-                           out_dtype, ldo, block_m, block_n, group_m, xcd,
-                           (staged_b ? MXGG_B_PAIRS : 0) | (staged_a ? MXGG_A_PAIRS : 0), part, wl.part, st);
+  return launch_grouped_mm(staged_a ? pa.dst : A, staged_a ? (int64_t)ldp : lda,
+                           plain ? A_s : (const uint8_t*)wsd, staged_b ? pb.dst : B, b_fmt,
+                           staged_b ? (int64_t)ldp : ldb_n, staged_b ? N * ldp : ldb_e,
+                           plain ? B_s : (const uint8_t*)(wsd + T * M), offs, E, M, N, K, out, out_dtype, ldo,
+                           block_m, block_n, group_m, xcd, (staged_b ? MXGG_B_PAIRS : 0) | (staged_a ? MXGG_A_PAIRS : 0),
+                           part, wl.part, st, plain, ldas, ldbs_n, ldbs_e);
 }
 
 extern "C" int mxgg_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, int64_t ldas,

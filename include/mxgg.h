@@ -234,6 +234,11 @@ int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, int b_fmt, in
  *            GEMM reads in whole 128-byte lines.  A workspace of exactly the
  *            recommended size stages nothing; staging never takes room from the
  *            partial tiles, and the output bits are the same either way.
+ *            A call that stages nothing, of at most 1.2e11 flop (2*M*N*K), on
+ *            scales whose rows and expert strides are 16-byte multiples at
+ *            16-byte aligned addresses, reads the plain scales directly (no
+ *            re-layout launch; the scale room of the workspace is still
+ *            required and left unused): the same bits.
  * K must be a multiple of 32.  A and B rows must be 16-byte aligned; scale
  * rows need no alignment.  Results do not depend on the workspace size beyond
  * fp32 summation order (a cut tile adds its pieces in a fixed order, so

@@ -87,7 +87,7 @@ def test_to_mx_both_and_dim0_match_oracle(gpu, dtype, shape):
             np.testing.assert_array_equal(bits_u8(d_q), cq)
 
 
-def _fwd_both_ways(gpu, E, M, N, K, offs, fp4=False, out_dtype=torch.bfloat16, seed=0):
+def _fwd_both_ways(gpu, E, M, N, K, offs, fp4=False, out_dtype=torch.bfloat16, seed=0, tile=None):
     import kernels
     g = torch.Generator(device=gpu).manual_seed(seed)
     a = torch.randn((M, K), device=gpu, generator=g).to(torch.bfloat16)
@@ -98,23 +98,34 @@ def _fwd_both_ways(gpu, E, M, N, K, offs, fp4=False, out_dtype=torch.bfloat16, s
     ta, _ = kernels.to_mx(a, scale_layout="steps")
     tw, _ = kernels.to_mx(w, elem_dtype=fp, scale_layout="steps")
     offs_t = torch.tensor(offs, dtype=torch.int32, device=gpu)
-    plain = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs_t, out_dtype=out_dtype)
-    steps = kernels.triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs_t, out_dtype=out_dtype)
+    kw = {} if tile is None else {"BLOCK_M": tile, "BLOCK_N": tile}
+    plain = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs_t, out_dtype=out_dtype, **kw)
+    steps = kernels.triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs_t, out_dtype=out_dtype, **kw)
     torch.cuda.synchronize()
     return plain, steps, (qa, sa, qw, sw)
 
 
-@pytest.mark.parametrize("E,M,N,K,fp4,out_dtype", [
-    (4, 1024, 512, 544, False, torch.bfloat16),      # K % 128 = 32: a padded last step
-    (3, 448, 200, 96, False, torch.float32),         # ragged N, unaligned output path
-    (4, 1024, 512, 512, True, torch.bfloat16),       # e2m1 weights
-    (8, 16640, 2048, 5120, False, torch.bfloat16),   # sweep shape whose last round is split
-    (1, 16640, 2048, 2048, False, torch.bfloat16),   # quarter-tile last round
+# Calls that stage nothing, of at most 1.2e11 flop, on plain to_mx scales
+# whose rows are 16-byte multiples (K a multiple of 512), run the plain-scale
+# kernels (no re-layout launch); the others re-lay the scales step-major.
+# The cases cover both, and every case compares with the step-major call bit
+# for bit.
+@pytest.mark.parametrize("E,M,N,K,fp4,out_dtype,tile", [
+    (4, 1024, 512, 544, False, torch.bfloat16, None),      # K % 128 = 32: a padded last step (re-layout)
+    (3, 448, 200, 96, False, torch.float32, None),         # ragged N, unaligned output path (re-layout)
+    (4, 1024, 512, 512, True, torch.bfloat16, None),       # plain: e2m1 weights, one partial 8-step piece
+    (8, 16640, 2048, 5120, False, torch.bfloat16, None),   # re-layout: sweep shape whose last round is split
+    (1, 16640, 2048, 2048, False, torch.bfloat16, None),   # re-layout: quarter-tile last round
+    (1, 2080, 2048, 2048, False, torch.bfloat16, 128),     # plain: 128 x 128 tiles (expert-parallel shard)
+    (2, 4096, 512, 4608, False, torch.float16, None),      # plain: 36 steps, the last 8-step piece half used
+    (2, 4096, 1024, 4608, False, torch.bfloat16, 256),     # plain: a lone round of 64-68 tiles, split in
+                                                           # pieces that start inside an 8-step piece
+    (1, 2304, 7936, 2048, False, torch.bfloat16, 256),     # plain: 279 tiles, a quarter-tile last round
 ])
-def test_fwd_steps_bit_identical(gpu, E, M, N, K, fp4, out_dtype):
+def test_fwd_steps_bit_identical(gpu, E, M, N, K, fp4, out_dtype, tile):
     offs = seeded_offs(E, M - M % 32, seed=E + N)
-    print(f"fwd steps E={E} M={M} N={N} K={K} fp4={fp4} offs={list(offs)}", flush=True)
-    plain, steps, (qa, sa, qw, sw) = _fwd_both_ways(gpu, E, M, N, K, offs, fp4, out_dtype, seed=K)
+    print(f"fwd steps E={E} M={M} N={N} K={K} fp4={fp4} tile={tile} offs={list(offs)}", flush=True)
+    plain, steps, (qa, sa, qw, sw) = _fwd_both_ways(gpu, E, M, N, K, offs, fp4, out_dtype, seed=K, tile=tile)
     rows = int(offs[-1])
     assert torch.equal(plain[:rows].view(torch.int16 if out_dtype != torch.float32 else torch.int32),
                        steps[:rows].view(torch.int16 if out_dtype != torch.float32 else torch.int32))
@@ -122,6 +133,31 @@ def test_fwd_steps_bit_identical(gpu, E, M, N, K, fp4, out_dtype):
         ref = O.grouped_mm(bits_u8(qa), bits_u8(sa), bits_u8(qw), bits_u8(sw), offs,
                            b_elem="e2m1" if fp4 else "e4m3")
         assert O.rel_fro(ref[:rows], steps[:rows].float().cpu().numpy()) <= 3e-3
+
+
+def test_fwd_plain_scales_padded_strides(gpu):
+    """Plain scales in row- and expert-padded buffers (strides 16 bytes past
+    the row and 48 bytes past the expert): the same bits as contiguous ones."""
+    import kernels
+    E, M, N, K = 3, 1536, 640, 2048
+    offs = seeded_offs(E, M, seed=5)
+    print(f"fwd padded plain scales E={E} M={M} N={N} K={K} offs={list(offs)}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(11)
+    a = torch.randn((M, K), device=gpu, generator=g).to(torch.bfloat16)
+    w = (torch.randn((E, N, K), device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    sa, qa = kernels.to_mx(a)
+    sw, qw = kernels.to_mx(w)
+    nb = K // 32
+    pa = torch.full((M, nb + 16), 255, dtype=torch.uint8, device=gpu)
+    pa[:, :nb] = sa.view(torch.uint8)
+    pw = torch.full((E * (N * (nb + 16) + 48),), 255, dtype=torch.uint8, device=gpu)
+    pw_v = torch.as_strided(pw, (E, N, nb), (N * (nb + 16) + 48, nb + 16, 1))
+    pw_v.copy_(sw.view(torch.uint8))
+    offs_t = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    want = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, offs_t)
+    got = kernels.triton_mxfp8_grouped_mm(qa, qw, pa[:, :nb].view(sa.dtype), pw_v.view(sw.dtype), offs_t)
+    torch.cuda.synchronize()
+    assert torch.equal(want.view(torch.int16), got.view(torch.int16))
 
 
 @pytest.mark.parametrize("E,M,N,K,offs", [
