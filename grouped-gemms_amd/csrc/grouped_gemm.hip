@@ -1846,15 +1846,23 @@ static size_t fwd_staging_bytes(int E, int64_t M, int64_t N, int64_t K, int b_fm
   return (size_t)E * (size_t)N * (size_t)staged_ld(K) + 256;
 }
 
+// Forward calls of at most this many multiply-adds (1.2e11 flop) that stage
+// nothing run on plain scales without a re-layout launch (run_grouped_mm).
+constexpr int64_t kPlainMaxMacs = (int64_t)60000000000;
+
 // The same for A (M, K), or 0: its copy's time over the GEMM's is about
 // 400 / N, and staging it paid at N >= 8192 on every sweep shape (drop-in
 // call, same box: -1 to -12% at E = 4 and 8, where the weight is not staged;
 // -0.1 to -6% at E = 1 and 2 on top of the staged weight; with e2m1
 // weights, BASELINE config 5 -2.7%), not reliably at N = 5120 (-6% to
-// +1.4%).  A is e4m3 whatever the weight's format.
+// +1.4%).  A is e4m3 whatever the weight's format.  Not on calls of at most
+// kPlainMaxMacs: their re-layout launch costs more than the row pairs save
+// (E = 1, M = 2080, N = 8192, K = 2048: 57.3 us staged, 52.6 us on plain
+// scales and row-major A).
 static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
   if ((b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1) || M <= 0 || M % 2 || N < 8192 || K < 2048) return 0;
   if (M / 2 > (1 << 22) || K >= (1 << 22)) return 0;   // launch grid, int offsets
+  if (M * N <= kPlainMaxMacs / K) return 0;
   return (size_t)M * (size_t)staged_ld(K) + 256;
 }
 
@@ -2322,8 +2330,6 @@ static int check_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* A_s, i
 
 // Plain to_mx scales the GEMMs can read directly (plain-scale kernels): rows
 // of 16-byte multiples, 16-byte aligned buffers, byte ranges below 2**31.
-constexpr int64_t kPlainMaxMacs = (int64_t)60000000000;   // 1.2e11 flop
-
 static bool plain_scales_ok(const uint8_t* A_s, int64_t ldas, const uint8_t* B_s, int64_t ldbs_n, int64_t ldbs_e,
                             int E, int64_t M, int64_t N) {
   if (ldas % 16 || ldbs_n % 16 || (E > 1 && ldbs_e % 16) || !aligned16(A_s) || !aligned16(B_s)) return false;

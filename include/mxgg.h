@@ -250,8 +250,9 @@ size_t mxgg_grouped_mm_workspace_size(int E, int64_t M, int64_t N, int64_t K);
  * mxgg_grouped_mm stages e4m3 operands in row pairs, or 0 where the copies
  * would not pay for themselves: B (E * N * K rounded up to 64, plus 256) for
  * E <= M / 8192 and K >= 4096, or K >= 2048 with N >= 4096 (e4m3 B only); A
- * (M * K rounded up to 64, plus 256) for N >= 8192, K >= 2048 and M even
- * (e4m3 or e2m1 B).  The copies then
+ * (M * K rounded up to 64, plus 256) for N >= 8192, K >= 2048, M even and
+ * M * N * K above 6e10 (e4m3 or e2m1 B; smaller calls skip the re-layout
+ * launch instead, see mxgg_grouped_mm).  The copies then
  * cost a few percent of the GEMM's time and save more.  No counterpart in the
  * reference, whose Triton kernel reads its operands where they lie.
  */

@@ -128,8 +128,11 @@ def test_grouped_mm_workspace_without_gpu():
     assert lib.mxgg_grouped_mm_staging_size(2, 16384, 5120, 5120, E4M3) == 2 * 5120 * 5120 + 256
     assert lib.mxgg_grouped_mm_staging_size(3, 16384, 5120, 5120, E4M3) == 0     # E > M / 8192
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 2048, 2048, E4M3) == 0     # K, N < 4096
-    # ... plus A (M * K rounded up to 64, plus 256) for N >= 8192, K >= 2048, M even
+    # ... plus A (M * K rounded up to 64, plus 256) for N >= 8192, K >= 2048, M even and
+    # M * N * K above 6e10 (smaller calls run on plain scales without a re-layout launch)
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 2048, E4M3) == 8192 * 2048 + 256 + 16640 * 2048 + 256
+    assert lib.mxgg_grouped_mm_staging_size(1, 2080, 8192, 2048, E4M3) == 0       # 3.5e10 multiply-adds
+    assert lib.mxgg_grouped_mm_staging_size(1, 3584, 8192, 2048, E4M3) == 3584 * 2048 + 256   # 6.01e10 multiply-adds
     assert lib.mxgg_grouped_mm_staging_size(8, 16640, 8192, 5120, E4M3) == 16640 * 5120 + 256   # A only
     assert lib.mxgg_grouped_mm_staging_size(8, 16641, 8192, 5120, E4M3) == 0                  # odd M
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 1024, E4M3) == 0     # K < 2048

@@ -289,7 +289,7 @@ def test_fwd_staged_weight_bitwise(gpu, case):
     stage = lib.mxgg_grouped_mm_staging_size(E, M, N, K, _lib.FMT_E4M3)
     ldp = (K + 63) // 64 * 64
     stage_b = E * N * ldp + 256 if E * 8192 <= M and (K >= 4096 or (K >= 2048 and N >= 4096)) else 0
-    stage_a = M * ldp + 256 if N >= 8192 and K >= 2048 and M % 2 == 0 else 0
+    stage_a = M * ldp + 256 if N >= 8192 and K >= 2048 and M % 2 == 0 and M * N * K > 6e10 else 0
     assert stage == stage_b + stage_a > 0
     offs = _odd_offs(E, M - 100, E + K) if kind == "odd" else \
         O.generate_jagged_offs(E, M, 32, rng=random.Random(E * 7 + N))
