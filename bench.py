@@ -98,17 +98,42 @@ def fwd_kernel_name(cfg: dict) -> str:
     N, B format, LDS stages>, pieces=false, bf16 epilogue.  A call may also
     launch the piece / quarter-tile / reduce kernels of a split last round;
     the kernel-only event time covers those too."""
-    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4>, false, 1>"
+    return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4, false>, false, 1>"
 
 
 # whole-tile kernels with the bf16 epilogue (template argument 1): the bench's outputs are bf16 with aligned rows
-WGRAD_KERNEL = "mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4>, false, 1>"
+WGRAD_KERNEL = "mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4, false>, false, 1>"
+
+
+def wgrad_kernel_name(E: int, M: int, N: int, K: int) -> str:
+    """Device-kernel name of the whole-tile kernel of a wgrad call of this
+    shape: 256 x 256 (WGRAD_KERNEL) or, where the library picks them
+    (mxgg_wgrad_config, needs the GPU), 128 x 128 tiles."""
+    import ctypes
+    from kernels import _lib
+    b = ctypes.c_int32(0)
+    _lib.check(_lib.load().mxgg_wgrad_config(E, M, N, K, ctypes.byref(b)))
+    return f"mxgg::wgrad_kernel<mxgg::Cfg<{b.value}, {b.value}, 2, 2, 0, 4, false>, false, 1>"
 
 
 def canon(kernel: str) -> str:
     """Kernel name without return type, arguments and blanks, for matching
-    names across demanglers (``> >`` vs ``>>``)."""
-    return kernel.replace("void ", "").split("(")[0].replace(" ", "")
+    names across demanglers (``> >`` vs ``>>``), and without the Cfg's scale
+    source argument where it is the default step-major one (``false``): the
+    names of summaries made before that argument existed match the same
+    kernels."""
+    k = kernel.replace("void ", "").split("(")[0].replace(" ", "")
+    return re.sub(r"(Cfg<\d+,\d+,\d+,\d+,\d+,\d+),false>", r"\1>", k)
+
+
+def gemm_launch(name: str):
+    """'whole' / 'piece' for a whole-tile / split-piece launch of the forward
+    or wgrad GEMM kernel (their last two template arguments: pieces, epilogue),
+    else None (quarter-tile, reduce and other kernels)."""
+    if not ("mxgg::fwd_kernel<" in name or "mxgg::wgrad_kernel<" in name):
+        return None
+    m = re.search(r">,\s*(true|false),\s*\d+>\s*$", name.replace("void ", "").split("(")[0])
+    return None if m is None else ("piece" if m.group(1) == "true" else "whole")
 
 
 def read_traffic(kernel: str):
@@ -212,7 +237,7 @@ def pmc_summary(fetch_csv: str, write_csv: str, steps: int, warmup: int, n_shape
         # whole-tile GEMM kernels only: one per call (piece / reduce kernels of a
         # split last round, when launched, are left out of the per-call match)
         scaled[counter] = [(n, v * factor * 1024.0) for _, n, v in rows
-                           if ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n]
+                           if gemm_launch(n) == "whole"]
     f, w = scaled["FETCH_SIZE"], scaled["WRITE_SIZE"]
     # each call is timed twice (plain scales, then step-major; with
     # --kernel-only step-major only), warmup + steps launches each; the
@@ -316,7 +341,7 @@ def call_spans(trace_csv: str):
     for t0, t1, name in rows:
         n = name.replace("void ", "").split("(")[0]
         if any(n.startswith(g) for g in GEMM_KERNELS):
-            whole = ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n
+            whole = gemm_launch(n) == "whole"
             if cur is not None and whole and cur[2]:
                 close()          # back-to-back calls: a call's whole-tile kernel comes first
                 cur = None
@@ -325,7 +350,7 @@ def call_spans(trace_csv: str):
             cur[1] = max(cur[1], t1)
             if whole:
                 cur[2] = n
-            elif ", true, " in n and ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n):
+            elif gemm_launch(n) == "piece":
                 cur[4] = re.sub(r", true, \d+>$", ", false, 1>", n)
         else:
             close()
@@ -353,8 +378,8 @@ def dropin_spans(trace_csv: str):
             j, g0, g1, whole, piece, reduced = i + 2, None, None, None, None, False
             while j < len(rows) and any(rows[j][2].startswith(g) for g in GEMM_KERNELS):
                 t0, t1, n = rows[j]
-                is_whole = ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n) and ", false" in n
-                is_piece = ", true, " in n and ("mxgg::fwd_kernel<" in n or "mxgg::wgrad_kernel<" in n)
+                is_whole = gemm_launch(n) == "whole"
+                is_piece = gemm_launch(n) == "piece"
                 # the next call's GEMM launches (unflushed warmup reps of the bench's next variant follow
                 # directly): a second whole-tile launch, or a piece launch after this call's reduce
                 if (is_whole and g0 is not None) or (is_piece and reduced):
@@ -666,7 +691,7 @@ def native_sweep(dev, args, flush, shapes, offs_by_shape, rows, account):
         if args.only in ("all", "wgrad"):
             tg, pg = to_mx_dim0(torch.randn((M, N), device=dev).to(torch.bfloat16), **lay)
             ti, pi = to_mx_dim0(torch.randn((M, K), device=dev).to(torch.bfloat16), **lay)
-            timed("wgrad_native_us", lambda: triton_mxfp8_wgrad(pg, tg, pi, ti, offs), WGRAD_KERNEL)
+            timed("wgrad_native_us", lambda: triton_mxfp8_wgrad(pg, tg, pi, ti, offs), wgrad_kernel_name(E, M, N, K))
             del tg, pg, ti, pi
         torch.cuda.empty_cache()
         log(json.dumps({"E": E, "N": N, "K": K, **{k: round(v, 1) for k, v in row.items() if k.endswith("_native_us")}}))
@@ -1042,7 +1067,8 @@ def main():
                                       args.steps, args.warmup, flush)
                 row["wgrad_us"] = med * 1e3
                 row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
-            kernel_only("wgrad_kernel_us", lambda: triton_mxfp8_wgrad(qg, tg, qi, ti, offs), WGRAD_KERNEL, flops, row)
+            kernel_only("wgrad_kernel_us", lambda: triton_mxfp8_wgrad(qg, tg, qi, ti, offs),
+                        wgrad_kernel_name(E, M, N, K), flops, row)
             del qg, qi, sg, si, tg, ti
         torch.cuda.empty_cache()
         rows.append(row)

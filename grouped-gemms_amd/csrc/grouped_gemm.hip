@@ -2648,6 +2648,29 @@ static int launch_wgrad_small(WgradParams p, bool al16, hipStream_t st) {
   return launch_status("wgrad");
 }
 
+// The plan of a wgrad call of `tiles` 256 x 256 tiles with `par` resident
+// workgroups and `slots` partial-tile slots (0: no room): the host plan, and
+// whether the kernels plan on the device and whether the call runs as 128 x
+// 128 whole tiles instead (launch_wgrad_small).
+struct WgradChoice {
+  Split sp;
+  bool dev;
+  bool small;
+};
+
+static WgradChoice wgrad_choice(int E, int64_t M, int64_t N, int64_t K, int64_t tiles, int par, int slots) {
+  constexpr int kib = CfgF8_256::BM * CfgF8_256::BN * 4 / 1024;
+  WgradChoice w{split_plan((int)tiles, par, (int)wgrad_group_steps(E, M), slots, kib), false, false};
+  // A lone round of several groups lasts as long as the longest group, which
+  // only the device knows: the kernels plan from the groups' lengths
+  // (wgrad_groups, or wgrad_plan past 64 groups) whenever a group of all M
+  // rows would be split.
+  w.dev = E > 1 && slots > 0 && split_plan((int)tiles, par, (int)cdiv(M, STEP) + 1, slots, kib).units > 0;
+  const int64_t tiles128 = (int64_t)E * cdiv(N, 128) * cdiv(K, 128);
+  w.small = (!w.dev && w.sp.units == 0 && 2 * tiles <= par) || (2 * tiles <= par && tiles128 >= 2 * par);
+  return w;
+}
+
 // The wgrad launches of a checked call on step-major scales (gs: GO [T][N],
 // is: IA [T][K] dwords); part / part_bytes: room for the fp32 partial tiles
 // of tiles cut along the tokens (none: no tile is cut).
@@ -2671,25 +2694,20 @@ static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, c
   // only a lone under-filled round is split (its tiles all start at once)
   const bool may_split = E == 1 || tiles < par;
   const int slots = part && may_split ? split_slots<C>(part_bytes) : 0;
-  constexpr int kib = C::BM * C::BN * 4 / 1024;
-  const Split sp = split_plan((int)tiles, par, (int)wgrad_group_steps(E, M), slots, kib);
+  const WgradChoice wc = wgrad_choice(E, M, N, K, tiles, par, slots);
+  const Split& sp = wc.sp;
   p.dp = sp.dp;
   p.S = sp.S;
   p.units = sp.units;
-  // A lone round of several groups lasts as long as the longest group, which
-  // only the device knows: the kernels plan from the groups' lengths
-  // (wgrad_groups, or wgrad_plan past 64 groups) whenever a group of all M
-  // rows would be split.  The grids cover any such plan: every tile whole, or
-  // at most min(par, slots) pieces and every tile reduced.
-  if (E > 1 && slots > 0 && split_plan((int)tiles, par, (int)cdiv(M, STEP) + 1, slots, kib).units > 0) {
+  // device plan: the grids cover any such plan, every tile whole, or at most
+  // min(par, slots) pieces and every tile reduced
+  if (wc.dev) {
     p.dev = 1;
     p.par = par;
     p.slots = slots;
   }
   const bool al16 = K % 8 == 0 && (uintptr_t)out % 16 == 0;
-  const int64_t tiles128 = (int64_t)E * cdiv(N, 128) * cdiv(K, 128);
-  if ((!p.dev && sp.units == 0 && 2 * tiles <= par) || (2 * tiles <= par && tiles128 >= 2 * par))
-    return launch_wgrad_small(p, al16, st);
+  if (wc.small) return launch_wgrad_small(p, al16, st);
   const int64_t whole_ub = p.dev ? tiles : sp.dp;
   const int64_t units_ub = p.dev ? slots : sp.units;
   const int64_t split_tiles_ub = p.dev ? tiles : (sp.units ? sp.units / sp.S : 0);
@@ -2711,6 +2729,24 @@ static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, c
   hipLaunchKernelGGL((wgrad_reduce_kernel<C>), dim3((unsigned)(split_tiles_ub * ReduceShape<C>::CH)), dim3(256),
                      0, st, p);
   return launch_status("wgrad");
+}
+
+extern "C" int mxgg_wgrad_config(int E, int64_t M, int64_t N, int64_t K, int* block) {
+  clear_error();
+  if (!block) return fail(MXGG_ERR_INVALID_ARG, "wgrad_config: null output pointer");
+  if (E <= 0 || E > 65535 || M < 0 || N <= 0 || K <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return fail(MXGG_ERR_INVALID_ARG, "wgrad_config: shape out of range");
+  typedef CfgF8_256 C;
+  const int64_t tiles = (int64_t)E * cdiv(N, C::BM) * cdiv(K, C::BN);
+  if (tiles > INT32_MAX / 2) return fail(MXGG_ERR_UNSUPPORTED, "wgrad_config: grid too large");
+  if (int rc = require_device()) return rc;
+  static int resident_cache[64];
+  const int par = resident_workgroups(wgrad_kernel<C, false>, C::NT, resident_cache);
+  if (par <= 0) return fail(MXGG_ERR_NO_DEVICE, "wgrad_config: resident workgroups unknown");
+  const size_t part = wgrad_part_cap(E, M, N, K);
+  const int slots = part && (E == 1 || tiles < par) ? split_slots<C>(part) : 0;
+  *block = wgrad_choice(E, M, N, K, tiles, par, slots).small ? 128 : 256;
+  return MXGG_OK;
 }
 
 extern "C" int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,

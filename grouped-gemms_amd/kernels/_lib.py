@@ -80,6 +80,7 @@ SIGNATURES = {
                                         ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i32)]),
     "mxgg_wgrad_workspace_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
     "mxgg_wgrad_staging_size": (_c_sz, [_c_i32, _c_i64, _c_i64, _c_i64]),
+    "mxgg_wgrad_config": (_c_i32, [_c_i32, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i32)]),
     "mxgg_wgrad": (_c_i32, [_c_p, _c_i64, _c_p, _c_i64,
                             _c_p, _c_i64, _c_p, _c_i64,
                             _c_p, _c_i32, _c_i64, _c_i64, _c_i64,

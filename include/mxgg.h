@@ -346,6 +346,18 @@ size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
  * or K, and for M not a multiple of 32.  No counterpart in the reference.
  */
 size_t mxgg_wgrad_staging_size(int E, int64_t M, int64_t N, int64_t K);
+/*
+ * Tile edge (256 or 128, into *block) of the GEMM launches of a mxgg_wgrad /
+ * mxgg_wgrad_steps call of this shape given the recommended workspace
+ * (mxgg_wgrad_workspace_size): 128 x 128 tiles where 256 x 256 tiles would
+ * fill at most half the chip and either no tile of them is cut along the
+ * tokens or 128 x 128 tiles fill at least one round; else 256 x 256.  Reads
+ * the device's resident workgroup count (MXGG_ERR_NO_DEVICE without one).
+ * Replaces the tile and split choice of `triton_mxfp8_wgrad`
+ * (kernels/backward.py:245-254), as mxgg_grouped_mm_config does the
+ * forward's.
+ */
+int mxgg_wgrad_config(int E, int64_t M, int64_t N, int64_t K, int* block);
 int mxgg_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* go_s, int64_t ld_gos,
                const uint8_t* ia_t, int64_t ld_ia, const uint8_t* ia_s, int64_t ld_ias,
                const int32_t* offs, int E, int64_t M, int64_t N, int64_t K,

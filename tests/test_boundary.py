@@ -208,6 +208,20 @@ def test_wgrad_out_dtypes_without_gpu():
     assert rc == _lib.ERR_INVALID_ARG and b"out_dtype" in lib.mxgg_last_error_string()
 
 
+def test_wgrad_config_without_gpu():
+    """mxgg_wgrad_config checks its arguments on the host, then needs the
+    device (its answer depends on the resident workgroup count)."""
+    import ctypes
+    from kernels import _lib
+    lib = _lib.load()
+    b = ctypes.c_int32(0)
+    assert lib.mxgg_wgrad_config(2, 16640, 2048, 2048, None) == _lib.ERR_INVALID_ARG
+    assert lib.mxgg_wgrad_config(0, 16640, 2048, 2048, ctypes.byref(b)) == _lib.ERR_INVALID_ARG
+    assert lib.mxgg_wgrad_config(2, 16640, 0, 2048, ctypes.byref(b)) == _lib.ERR_INVALID_ARG
+    assert lib.mxgg_wgrad_config(2, 16640, 2048, 2048, ctypes.byref(b)) == _lib.ERR_NO_DEVICE
+    assert b.value == 0
+
+
 def test_noalloc_rejects_calls_beyond_the_array_without_gpu():
     """mxgg_grouped_mm_noalloc rejects a call whose re-laid scales,
     4 * cdiv(K, 128) * (M + E*N) bytes, exceed its device array with

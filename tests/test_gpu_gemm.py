@@ -318,6 +318,24 @@ def _wgrad_case(E, M, N, K, offs, gpu, seed=0, out_dtype=torch.bfloat16):
     return out, ref, go, ia
 
 
+@pytest.mark.parametrize("E,M,N,K,block", [
+    (2, 16640, 2048, 2048, 128),    # 128 tiles of 256 (half a round, split) -> 512 of 128 fill a round
+    (1, 16640, 2048, 2048, 256),    # 64 tiles, split along 130 steps; 256 tiles of 128 would not fill a round
+    (1, 2080, 2048, 2048, 128),     # 17 steps: too short to split, 64 tiles of 256
+    (4, 16640, 2048, 2048, 256),    # 256 tiles: a full round
+    (8, 16640, 8192, 8192, 256),
+])
+def test_wgrad_config_tiles(gpu, E, M, N, K, block):
+    """mxgg_wgrad_config on MI355X (256 CUs, one 256 x 256 workgroup each)."""
+    import ctypes
+    from kernels import _lib
+    if torch.cuda.get_device_properties(gpu).multi_processor_count != 256:
+        pytest.skip("expected tile choices are for 256 CUs")
+    b = ctypes.c_int32(0)
+    _lib.check(_lib.load().mxgg_wgrad_config(E, M, N, K, ctypes.byref(b)))
+    assert b.value == block
+
+
 @pytest.mark.parametrize("E,M,N,K", [(4, 1024, 512, 512), (1, 1024, 256, 384), (8, 2048, 512, 256)])
 def test_wgrad_random(gpu, E, M, N, K):
     offs = seeded_offs(E, M, seed=M + E)
