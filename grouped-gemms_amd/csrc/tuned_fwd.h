@@ -8,7 +8,7 @@
 // swept shape).  Fields: E, M, N, K, b_fmt (0 e4m3, 4 e2m1), block_m, block_n,
 // group_m, xcd swizzle, split (1: the last round may be split along K when
 // the workspace allows it, 0: whole tiles only).
-// sweep: 18 shapes (e4m3, 3 offset draws), 10 with a gain of at least 2% on every draw; AMD Radeon Graphics
+// sweep: 36 shapes (e4m3, 3 offset draws), 14 with a gain of at least 2% on every draw; AMD Radeon Graphics
 static const TunedFwd kTunedFwd[] = {
     {1, 16640, 2048, 2048, 0, 256, 256, 1, 8, 1},   // 95.3 us
     {1, 16640, 2048, 8192, 0, 256, 256, 4, 1, 1},   // 262.8 us
@@ -20,5 +20,9 @@ static const TunedFwd kTunedFwd[] = {
     {2, 16640, 2048, 8192, 0, 256, 256, 4, 1, 1},   // 273.2 us
     {2, 16640, 8192, 2048, 0, 256, 256, 1, 1, 1},   // 291.8 us
     {2, 16640, 8192, 5120, 0, 256, 256, 1, 1, 0},   // 636.3 us
+    {4, 16640, 8192, 5120, 0, 256, 256, 1, 1, 1},   // 630.8 us
+    {4, 16640, 8192, 8192, 0, 256, 256, 1, 1, 1},   // 973.6 us
+    {8, 16640, 5120, 2048, 0, 256, 256, 4, 8, 1},   // 200.9 us
+    {8, 16640, 8192, 2048, 0, 256, 256, 1, 1, 1},   // 286.5 us
     {0, 0, 0, 0, 0, 0, 0, 0, 0, 0},   // end
 };
