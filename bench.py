@@ -305,10 +305,13 @@ def counter_summary(csv_path: str) -> str:
         a[0] += float(r["Counter_Value"])
         a[1] += 1
     names = sorted({c for v in acc.values() for c in v})
-    out = [f"{'kernel':62s} " + " ".join(f"{c:>16s}" for c in names) + f" {'dispatches':>10s}"]
+    # full kernel names: the trailing template arguments (pieces, epilogue)
+    # tell the launches of one configuration apart
+    w = max([62] + [len(n) for n in acc])
+    out = [f"{'kernel':{w}s} " + " ".join(f"{c:>16s}" for c in names) + f" {'dispatches':>10s}"]
     for n, v in sorted(acc.items()):
         cells = " ".join(f"{v[c][0] / v[c][1]:16.4f}" if c in v else f"{'-':>16s}" for c in names)
-        out.append(f"{n[:62]:62s} {cells} {max(x[1] for x in v.values()):10d}")
+        out.append(f"{n:{w}s} {cells} {max(x[1] for x in v.values()):10d}")
     return "\n".join(out)
 
 
