@@ -124,19 +124,22 @@ def test_fwd_empty_reduction_gives_zeros(gpu):
     dummy = torch.zeros(4096, dtype=torch.uint8, device=gpu)   # holds every row range the calls name
     offs = torch.tensor([40, 80], dtype=torch.int32, device=gpu)
     stream = torch.cuda.current_stream().cuda_stream
-    for steps in (False, True):
+    # step-major scales; plain scales with 1-byte rows (re-layout path); plain scales with 16-byte rows (read by the
+    # GEMM itself: 96 * 16 and 2 * 64 * 16 bytes, inside the dummy buffer)
+    for mode in ("steps", "plain", "plain16"):
         out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
         p = dummy.data_ptr()
-        if steps:
+        if mode == "steps":
             rc = lib.mxgg_grouped_mm_steps(p, 16, p, p, 0, 16, 16 * N, p, offs.data_ptr(), E, M, N, 0,
                                            out.data_ptr(), 0, N, 0, 0, 0, 0, 0, None, 0, stream)
         else:
-            rc = lib.mxgg_grouped_mm(p, 16, p, 1, p, 0, 16, 16 * N, p, 1, N, offs.data_ptr(), E, M, N, 0,
+            ls = 1 if mode == "plain" else 16
+            rc = lib.mxgg_grouped_mm(p, 16, p, ls, p, 0, 16, 16 * N, p, ls, ls * N, offs.data_ptr(), E, M, N, 0,
                                      out.data_ptr(), 0, N, 0, 0, 0, 0, None, 0, stream)
         _lib.check(rc)
         torch.cuda.synchronize()
-        assert not out[:80].float().abs().sum().item(), f"steps={steps}"
-        assert out[80:].float().isnan().all(), f"steps={steps}"
+        assert not out[:80].float().abs().sum().item(), mode
+        assert out[80:].float().isnan().all(), mode
 
 
 @pytest.mark.parametrize("N,K", [(200, 96), (33, 160), (4096, 32)])
