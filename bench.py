@@ -92,13 +92,22 @@ def time_call(fn, steps: int, warmup: int, flush_buf):
     return statistics.median(ts), sum(ts) / len(ts)
 
 
-def fwd_kernel_name(cfg: dict) -> str:
+def fwd_kernel_name(cfg: dict, rows: bool = False) -> str:
     """Device-kernel name (as rocprofv3 lists it) of the whole-tile kernel of an
-    e4m3 forward/dgrad launch: Cfg<BLOCK_M, BLOCK_N, waves along M, waves along
-    N, B format, LDS stages>, pieces=false, bf16 epilogue.  A call may also
-    launch the piece / quarter-tile / reduce kernels of a split last round;
-    the kernel-only event time covers those too."""
+    e4m3 forward/dgrad launch on step-major scales: Cfg<BLOCK_M, BLOCK_N, waves
+    along M, waves along N, B format, LDS stages, plain scales>, pieces=false,
+    bf16 epilogue; with ``rows`` (row-major A), the 256 x 256 tiles run as
+    XLine (A in two-stage LDS slots, 3 of them).  A call may also launch the
+    piece / quarter-tile / reduce kernels of a split last round; the
+    kernel-only event time covers those too."""
+    if rows and cfg["BLOCK_M"] == 256:
+        return XLINE_KERNEL
     return f"mxgg::fwd_kernel<mxgg::Cfg<{cfg['BLOCK_M']}, {cfg['BLOCK_N']}, 2, 2, 0, 4, false>, false, 1>"
+
+
+# the 256 x 256 e4m3 forward whole-tile kernels: A in row pairs, and row-major A (XLine)
+FWD_KERNEL = "mxgg::fwd_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4, false>, false, 1>"
+XLINE_KERNEL = "mxgg::fwd_kernel<mxgg::XLine<mxgg::Cfg<256, 256, 2, 2, 0, 3, false> >, false, 1>"
 
 
 # whole-tile kernels with the bf16 epilogue (template argument 1): the bench's outputs are bf16 with aligned rows
@@ -159,7 +168,7 @@ def read_trace_avg(kernel: str, native: bool):
     path = os.path.join(ROOT, "profiles", "kernel_stats_sweep.txt")
     if not os.path.exists(path):
         return None
-    pat = (r"the native sweep's (\d+) after them: avg\s+([\d.]+) us" if native
+    pat = (r"the native sweep's (\d+)(?: after them)?: avg\s+([\d.]+) us" if native
            else r"the sweep's first (\d+): avg\s+([\d.]+) us")
     for line in open(path):
         head = line.strip().split("all calls")[0].strip()
@@ -174,7 +183,8 @@ def read_dropin_gemm(kernel: str):
     """The drop-in calls' figures of `kernel` in the committed kernel-trace
     summary (profiles/kernel_stats_sweep.txt: the GEMM launches the sweep's
     timed drop-in calls make, on operands staged in row pairs where the
-    library stages them, without and with their re-layout launch), or None."""
+    library stages them, without and with their re-layout launch; a line
+    may cover several whole-tile kernels, "A and B"), or None."""
     path = os.path.join(ROOT, "profiles", "kernel_stats_sweep.txt")
     if not os.path.exists(path):
         return None
@@ -182,8 +192,9 @@ def read_dropin_gemm(kernel: str):
            r".*re-layout launch \(([\d.]+) us\) ([\d.]+) TFLOP/s = ([\d.]+)")
     for line in open(path):
         m = re.search(pat, line)
-        if m and canon(m.group(2)) == canon(kernel):
-            return {"calls": int(m.group(1)), "gemm_us": float(m.group(3)), "achieved": float(m.group(4)),
+        if m and canon(kernel) in {canon(n) for n in m.group(2).split(" and ")}:
+            return {"calls": int(m.group(1)), "kernels": m.group(2).split(" and "),
+                    "gemm_us": float(m.group(3)), "achieved": float(m.group(4)),
                     "frac": float(m.group(5)), "relayout_us": float(m.group(6)),
                     "achieved_with_relayout": float(m.group(7)), "frac_with_relayout": float(m.group(8)),
                     "source": "profiles/kernel_stats_sweep.txt: rocprofv3 kernel-trace spans of the GEMM launches "
@@ -368,9 +379,9 @@ def dropin_spans(trace_csv: str):
     follow the bench's cache flush (its timed drop-in reps): the scale
     re-layout launch (which also stages operands in row pairs where the
     library does), then the call's GEMM dispatches.  Returns {whole-tile
-    kernel of the call: [(re-layout ns, GEMM span ns), ...]} in trace order;
-    a call whose every tile is split counts under the whole-tile kernel of its
-    configuration."""
+    kernel of the call: [(re-layout ns, GEMM span ns, start ns), ...]} in
+    trace order; a call whose every tile is split counts under the whole-tile
+    kernel of its configuration."""
     import csv
     rows = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"].replace("void ", "").split("(")[0])
                   for r in csv.DictReader(open(trace_csv)))
@@ -396,7 +407,7 @@ def dropin_spans(trace_csv: str):
                 reduced = reduced or "_reduce_kernel<" in n
                 j += 1
             if (whole or piece) and g0 is not None:
-                out.setdefault(whole or piece, []).append((relayout, g1 - g0))
+                out.setdefault(whole or piece, []).append((relayout, g1 - g0, rows[i][0]))
             i = j
         else:
             i += 1
@@ -486,12 +497,13 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
             text = (f"  {name:62s} all calls {len(v):6d}: avg {sum(t for t, _ in v) / len(v) / 1e3:9.2f} us;  "
                     f"right after the cache flush {len(cold):6d}: avg "
                     f"{(sum(cold) / len(cold) / 1e3) if cold else float('nan'):9.2f} us")
-            nb = bench_calls.get(canon(name))
+            nb = bench_calls.get(canon(name), 0)
             if nb and len(cold) >= nb:
                 text += f";  the sweep's first {nb}: avg {sum(cold[:nb]) / nb / 1e3:9.2f} us"
-                nn = native_calls.get(canon(name))
-                if nn and len(cold) >= nb + nn:
-                    text += f";  the native sweep's {nn} after them: avg {sum(cold[nb:nb + nn]) / nn / 1e3:9.2f} us"
+            nn = native_calls.get(canon(name))
+            if nn and len(cold) >= nb + nn and (nb == 0 or len(cold) >= nb):
+                text += (f";  the native sweep's {nn}{' after them' if nb else ''}: avg "
+                         f"{sum(cold[nb:nb + nn]) / nn / 1e3:9.2f} us")
             out.append(text)
     if trace_csv and line and line.get("roofline"):
         # the GEMM launches the drop-in calls make, on the operands as the
@@ -504,20 +516,26 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
         out += ["", "Drop-in calls, from the same trace: each timed rep's scale re-layout launch (with any operand "
                     "staging) and the span of its GEMM launches:"]
         for name, v in sorted(spans.items()):
-            out.append(f"  {name:62s} calls {len(v):6d}: re-layout avg {sum(a for a, _ in v) / len(v) / 1e3:8.2f} us, "
-                       f"GEMM span avg {sum(b for _, b in v) / len(v) / 1e3:9.2f} us")
+            out.append(f"  {name:62s} calls {len(v):6d}: re-layout avg {sum(x[0] for x in v) / len(v) / 1e3:8.2f} us, "
+                       f"GEMM span avg {sum(x[1] for x in v) / len(v) / 1e3:9.2f} us")
+        # the kernel-only sweep's forward + dgrad calls all run the dominant
+        # kernel; their drop-in twins run it or, where the call stages A in row
+        # pairs, the one-stage 256 x 256 kernel: both, in trace order
         for key in (rf["kernel"], WGRAD_KERNEL):
-            v = spans.get(key) or spans.get(next((k for k in spans if canon(k) == canon(key)), ""), [])
+            fam = (FWD_KERNEL, XLINE_KERNEL) if canon(key) in (canon(FWD_KERNEL), canon(XLINE_KERNEL)) else (key,)
+            v = sorted((x for k, xs in spans.items() if canon(k) in {canon(f) for f in fam} for x in xs),
+                       key=lambda x: x[2])
             bk = rf["by_kernel"].get(key)
             if not bk or len(v) < bk["launches"]:
                 continue
             nb = bk["launches"]
             flops = bk["tflops"] * 1e12 * bk["avg_launch_us"] * 1e-6
-            gem = sum(b for _, b in v[:nb]) / nb
-            rel = sum(a for a, _ in v[:nb]) / nb
+            gem = sum(x[1] for x in v[:nb]) / nb
+            rel = sum(x[0] for x in v[:nb]) / nb
             ach = flops / (gem * 1e-9) / 1e12
             whole_call = flops / ((gem + rel) * 1e-9) / 1e12
-            out.append(f"  the sweep's {nb} drop-in calls of {key}: GEMM launches {gem / 1e3:.2f} us = {ach:.1f} "
+            label = " and ".join(fam)
+            out.append(f"  the sweep's {nb} drop-in calls of {label}: GEMM launches {gem / 1e3:.2f} us = {ach:.1f} "
                        f"TFLOP/s = {ach / PEAK_MXFP8_TFLOPS:.3f} of {PEAK_MXFP8_TFLOPS} (dense MXFP8); with the "
                        f"re-layout launch ({rel / 1e3:.2f} us) {whole_call:.1f} TFLOP/s = "
                        f"{whole_call / PEAK_MXFP8_TFLOPS:.3f}")
@@ -1039,7 +1057,7 @@ def main():
                 if "bf16_us" in row:
                     row["fwd_speedup_vs_bf16"] = row["bf16_us"] / row["fwd_us"]
             kernel_only("fwd_kernel_us", lambda: triton_mxfp8_grouped_mm(qa, qw, ta, tw, offs),
-                        fwd_kernel_name(_pick_config(E, M, N, K)), flops, row)
+                        fwd_kernel_name(_pick_config(E, M, N, K), rows=True), flops, row)
             del qa, qw, sa, sw, ta, tw
         if args.only in ("all", "dgrad"):
             go = torch.randn((M, N), device=dev).to(torch.bfloat16)
@@ -1055,7 +1073,7 @@ def main():
                 row["dgrad_us"] = med * 1e3
                 row["dgrad_tflops"] = flops / (med * 1e-3) / 1e12
             kernel_only("dgrad_kernel_us", lambda: triton_mxfp8_grouped_mm(qg, qt, tg, tt, offs),
-                        fwd_kernel_name(_pick_config(E, M, K, N)), flops, row)
+                        fwd_kernel_name(_pick_config(E, M, K, N), rows=True), flops, row)
             del qg, qt, sg, st_, tg, tt
         if args.only in ("all", "wgrad"):
             go = torch.randn((M, N), device=dev).to(torch.bfloat16)

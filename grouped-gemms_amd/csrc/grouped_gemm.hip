@@ -142,6 +142,7 @@ struct Cfg {
   // to_mx scales (row r's byte b at r * ld + b, ld a multiple of 16), read
   // directly in 32-byte row pieces of 8 steps.
   static constexpr bool PS = PS_;
+  static constexpr bool XD = false;     // X in two-stage slots (XLine)
   static constexpr bool F4 = WFMT == MXGG_FMT_E2M1;
   static constexpr int NW = WGM * WGN;
   static constexpr int NT = NW * kWave;
@@ -188,6 +189,29 @@ struct Cfg {
   // issued no earlier than the group
   static_assert(NS <= GSTAGES + 1, "ring deeper than the scale prefetch");
   static_assert((NS - 1) * LPS + 2 * (PS ? SPW : 1) <= 63, "vmcnt range");
+};
+
+// Configuration B with X in two-stage slots.  A row-major X row gives a
+// stage 64 bytes, half a 128-byte line, so the one-stage ring copies each X
+// line in two requests.  X slot q here holds stages 2q and 2q+1 of every
+// tile row as one 128-byte piece, copied as whole lines; W keeps one-stage
+// slots.  B::NS slots of each, in two regions (256 x 256 tiles: X 96 KB,
+// W 48 KB), then the step-major scale ring.  Slot layout: tile row m at
+// byte 128 m, its 16-byte unit u (stage 2q + u / 4, elements 16 (u % 4) ..
+// +15 of it) at unit u ^ (m % 8) ^ ((m / 8) % 2): one unit over 8 consecutive
+// rows hits 8 different 16-byte bank groups of 128 bytes, and over 16
+// consecutive rows 16 different ones of 256 bytes.
+template <class B>
+struct XLine : B {
+  static constexpr bool XD = true;
+  static constexpr int XSLOT = 2 * B::XBYTES;
+  static constexpr int WOFF = B::NS * XSLOT;
+  static constexpr int SOFF = WOFF + B::NS * B::WBYTES;
+  static constexpr int LDS = SOFF + 2 * B::SSLOT;
+  static_assert(!B::PS && !B::F4 && B::NS == 3, "two-stage X slots: e4m3, step-major scales, 3 slots");
+  static_assert(B::QX % 2 == 0, "even and odd X copies alternate in a half pair");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(3 * B::QX + 2 * B::QW + 2 <= 63, "vmcnt range");
 };
 
 // 16-byte chunk swizzles: bijective on the chunk index for every 8-row and
@@ -271,9 +295,14 @@ struct Frags {
 // lane l holds 16 bytes of row l / 2 of the copy, the half (l ^ (l >> 4)) & 1
 // of the row's 32-byte piece, at byte s_base + i * s_step + 4 t of that
 // operand's scales for the piece starting at step t.
+// Two-stage X slots (C::XD): copy c of a pair covers tile rows 8c .. 8c+7
+// (128 bytes each), lane l row l / 8 of the copy and slot unit l % 8, which
+// holds unit (l % 8) ^ (l / 8) of the row's piece for even c (xoff) and
+// that ^ 1 for odd c (xoff2).
 template <class C>
 struct Plan {
   uint32_t xoff;
+  uint32_t xoff2;
   uint32_t woff;
   uint32_t s_base;
   uint32_t s_step;
@@ -283,10 +312,16 @@ template <class C>
 __device__ __forceinline__ void make_plan(Plan<C>& P, const Operand& X, const Operand& W,
                                           const ScaleSrc& xs, const ScaleSrc& ws) {
   const int lane = threadIdx.x % kWave;
-  {
+  if constexpr (C::XD) {
+    const int row = lane / 8;
+    const int ue = (lane & 7) ^ row, uo = ue ^ 1;
+    P.xoff = operand_off(X, (uint32_t)row, (uint32_t)ue * 16u) | ((uint32_t)ue << 28);
+    P.xoff2 = operand_off(X, (uint32_t)row, (uint32_t)uo * 16u) | ((uint32_t)uo << 28);
+  } else {
     const int row = lane / 4;
     const int c = (lane & 3) ^ swz4(row);
     P.xoff = operand_off(X, (uint32_t)row, (uint32_t)c * 16u) | ((uint32_t)c << 28);
+    P.xoff2 = 0;
   }
   if constexpr (C::F4) {
     const int row = lane / 2;
@@ -639,6 +674,187 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[C::FM][C::FN]) {
     for (int j = 0; j < C::FN; ++j) acc[i][j] = (v16f){};
 }
 
+// ---------------------------------------------------------------------------
+// Main loop with X in two-stage slots (XLine).  Stage r of the run (stage
+// s0 + r, s0 even) issues the copies of W stage r + 3 into W slot r % 3 and
+// of half (r + 1) & 1 of X pair q = (r + 5) / 2 (stages 2q, 2q+1) into X slot
+// q % 3, the slot of pair (r - 1) / 2, whose stages the waves have read by
+// the stage's barrier; the prologue copies pairs 0 and 1, half 0 of pair 2 and
+// W stages 0 .. 2.  Every full stage thus issues QX + QW copies, and the wait
+// before reading stage r + 1 (W copies two stages earlier, X copies three or
+// more) allows the previous stage's copies in flight.
+// ---------------------------------------------------------------------------
+
+// Half h of the X copies of the pair whose first stage is st (even) into X
+// slot xb; the chunk bounds as in issue_stage.
+template <class C>
+__device__ __forceinline__ void issue_xhalf(uint8_t* xb, const Operand& X, const Plan<C>& P, int st, int h,
+                                            int lo, int hi) {
+  const int wave = wave_id();
+  const int kk = st * BKS;
+  const int xlo = lo - kk <= 0 ? 0 : (lo - kk + 15) / 16;
+  const int xhi = hi - kk <= 0 ? 0 : (hi - kk) / 16;
+  const int ue = (int)(P.xoff >> 28), uo = (int)(P.xoff2 >> 28);
+  const uint32_t xe = (ue >= xlo && ue < xhi) ? (P.xoff & 0x0fffffffu) : kOOB;
+  const uint32_t xo = (uo >= xlo && uo < xhi) ? (P.xoff2 & 0x0fffffffu) : kOOB;
+  const int c0 = (wave * 2 + h) * C::QX;   // first copy (even)
+#pragma unroll
+  for (int i = 0; i < C::QX; ++i) {
+    const uint32_t so = ((uint32_t)st * C::XROW << X.pl) + (uint32_t)((c0 + i) * 8) * X.ld;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(X.data, (lds_ptr_t)(xb + (c0 + i) * 1024), 16, (i & 1) ? xo : xe, so,
+                                             0, 0);
+  }
+}
+
+// W copies of stage st into W slot wb (issue_stage's W part, e4m3).
+template <class C>
+__device__ __forceinline__ void issue_wstage(uint8_t* wb, const Operand& W, const Plan<C>& P, int st, int lo,
+                                             int hi) {
+  const int wave = wave_id();
+  const int kk = st * BKS;
+  const int wlo = lo - kk <= 0 ? 0 : (lo - kk + 15) / 16;
+  const int whi = hi - kk <= 0 ? 0 : (hi - kk) / 16;
+  const int wc = (int)(P.woff >> 28);
+  const uint32_t wo = (wc >= wlo && wc < whi) ? (P.woff & 0x0fffffffu) : kOOB;
+#pragma unroll
+  for (int i = 0; i < C::QW; ++i) {
+    const int q = wave * C::QW + i;
+    const uint32_t so = ((uint32_t)st * C::WROW << W.pl) + (uint32_t)(q * 16) * W.ld;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(W.data, (lds_ptr_t)(wb + q * 1024), 16, wo, so, 0, 0);
+  }
+}
+
+// read_stage for two-stage X slots: the stage of parity h2 of X slot xb, the
+// W stage in wb, step u of the scale group in ss.
+template <class C>
+__device__ __forceinline__ void read_stage_xd(const uint8_t* xb, const uint8_t* wb, const uint8_t* ss, int u, int h2,
+                                              Frags<C>& F, uint32_t (&xs)[C::FM], uint32_t (&ws)[C::FN]) {
+  const int wave = wave_id();
+  const int lane = threadIdx.x % kWave;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  const int hsel = lane >> 5;
+  const int r32 = lane & 31;
+  const int g = (r32 & 7) ^ ((r32 >> 3) & 1);
+  const int x0 = ((h2 << 2) | hsel) ^ g;        // elements 16 hsel .. +15
+  const int x1 = ((h2 << 2) | 2 | hsel) ^ g;    // elements 32 + 16 hsel .. +15
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+    const uint8_t* row = xb + (wm * C::WTM + i * 32 + r32) * 128;
+    v4i lo = *reinterpret_cast<const v4i*>(row + x0 * 16);
+    v4i hi = *reinterpret_cast<const v4i*>(row + x1 * 16);
+    F.b[i] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  const int sw = swz4(r32);
+  const int c0 = hsel ^ sw;
+  const int c1 = (2 + hsel) ^ sw;
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const uint8_t* row = wb + (wn * C::WTN + j * 32 + r32) * C::WROW;
+    v4i lo = *reinterpret_cast<const v4i*>(row + c0 * 16);
+    v4i hi = *reinterpret_cast<const v4i*>(row + c1 * 16);
+    F.a[j] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  const uint32_t* sx = reinterpret_cast<const uint32_t*>(ss) + u * C::BM;
+  const uint32_t* sy = reinterpret_cast<const uint32_t*>(ss) + C::GSTEPS * C::BM + u * C::BN;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) xs[i] = sx[wm * C::WTM + i * 32 + r32];
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) ws[j] = sy[wn * C::WTN + j * 32 + r32];
+}
+
+// One stage of the two-stage-X ring, as ring_stage: multiply stage s0 + r,
+// read stage s0 + r + 1, issue the copies described above.  TAIL: kXdFull;
+// kXdNoCopy1 / kXdNoCopy0, the third and second stage from the end, issue
+// nothing and wait for the copies of one / no later stage; kXdLast only
+// multiplies.
+constexpr int kXdFull = 0, kXdNoCopy1 = 1, kXdNoCopy0 = 2, kXdLast = 3;
+template <class C, bool FIRST = false, int TAIL = kXdFull>
+__device__ __forceinline__ void ring_stage_xd(uint8_t* smem, const Operand& X, const Operand& W,
+                                              __amdgpu_buffer_rsrc_t ssr, const Plan<C>& P, int s0, int r,
+                                              int lo, int hi, Frags<C>& Fc, uint32_t (&xc)[C::FM],
+                                              uint32_t (&wc)[C::FN], Frags<C>& Fn, uint32_t (&xn)[C::FM],
+                                              uint32_t (&wn)[C::FN], v16f (&acc)[C::FM][C::FN]) {
+  constexpr int NMMA = C::FM * C::FN;
+  constexpr int NE = NMMA >= 8 ? 2 : 1;
+  constexpr int NDS = C::FM * 2 + C::FN * 2 + C::FM + C::FN;
+  const int rn = r + 1;
+  const uint8_t* xnx = smem + ((rn >> 1) % C::NS) * C::XSLOT;
+  const uint8_t* wnx = smem + C::WOFF + (rn % C::NS) * C::WBYTES;
+  const uint8_t* snx = smem + C::SOFF + ((rn / C::GSTAGES) & 1) * C::SSLOT;
+  if constexpr (TAIL == kXdLast) {
+    mfma_range<C, 0, NMMA, FIRST>(Fc, xc, wc, acc);
+    hold(Fc, xc, wc);
+    MXGG_SCHED_FENCE();
+    return;
+  }
+  mfma_range<C, 0, NE, FIRST>(Fc, xc, wc, acc);
+  MXGG_SCHED_FENCE();
+  if constexpr (TAIL == kXdNoCopy0)
+    MXGG_WAIT_VM(0);
+  else
+    MXGG_WAIT_VM(C::LPS);
+  MXGG_BARRIER();
+  MXGG_SCHED_FENCE();
+  read_stage_xd<C>(xnx, wnx, snx, (rn / 2) % C::GSTEPS, rn & 1, Fn, xn, wn);
+  if constexpr (TAIL == kXdFull) {
+    const int tg = s0 / 2 + (rn / C::GSTAGES + 1) * C::GSTEPS;
+    uint8_t* sn = smem + C::SOFF + ((rn / C::GSTAGES + 1) & 1) * C::SSLOT;
+    issue_scales<C>(sn, ssr, P, tg, rn % C::GSTAGES == 0 && tg * STEP < hi);
+    const int q = (r + 5) >> 1;
+    issue_xhalf<C>(smem + (q % C::NS) * C::XSLOT, X, P, s0 + 2 * q, (r + 1) & 1, lo, hi);
+    issue_wstage<C>(smem + C::WOFF + (r % C::NS) * C::WBYTES, W, P, s0 + r + 3, lo, hi);
+  }
+  mfma_range<C, NE, NMMA, FIRST>(Fc, xc, wc, acc);
+  interleave_step<0, NMMA - NE, (NMMA - NE) / 2, NDS, TAIL == kXdFull ? C::LPS : 0>();
+  MXGG_SCHED_FENCE();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  finish_scales<C>(xn, wn, s0 + rn, lo, hi);
+  hold(Fc, xc, wc);
+  MXGG_SCHED_FENCE();
+}
+
+// ring_mainloop for two-stage X slots (the same range, padding and ZSTART
+// meaning; a run of n stages runs n rounded up to even, at least 6).
+template <class C, bool ZSTART>
+__device__ __forceinline__ void ring_mainloop_xd(uint8_t* smem, const Operand& X, const Operand& W,
+                                                 const ScaleSrc& xss, const ScaleSrc& wss, int s0, int s1,
+                                                 int lo, int hi, v16f (&acc)[C::FM][C::FN]) {
+  if (s0 >= s1) s1 = s0 + 1;
+  s0 &= ~1;
+  Plan<C> P;
+  make_plan<C>(P, X, W, xss, wss);
+  const __amdgpu_buffer_rsrc_t ssr = wave_id() < C::NSX ? xss.rsrc : wss.rsrc;
+  issue_scales<C>(smem + C::SOFF, ssr, P, s0 / 2, true);
+  issue_scales<C>(smem + C::SOFF + C::SSLOT, ssr, P, s0 / 2 + C::GSTEPS, true);
+  issue_xhalf<C>(smem, X, P, s0, 0, lo, hi);
+  issue_xhalf<C>(smem, X, P, s0, 1, lo, hi);
+  issue_wstage<C>(smem + C::WOFF, W, P, s0, lo, hi);
+  issue_xhalf<C>(smem + C::XSLOT, X, P, s0 + 2, 0, lo, hi);
+  issue_xhalf<C>(smem + C::XSLOT, X, P, s0 + 2, 1, lo, hi);
+  issue_wstage<C>(smem + C::WOFF + C::WBYTES, W, P, s0 + 1, lo, hi);
+  issue_xhalf<C>(smem + 2 * C::XSLOT, X, P, s0 + 4, 0, lo, hi);
+  issue_wstage<C>(smem + C::WOFF + 2 * C::WBYTES, W, P, s0 + 2, lo, hi);
+  MXGG_WAIT_VM(3 * C::QX + 2 * C::QW);   // pair 0 and W stage 0 (and the scales before them)
+  MXGG_BARRIER();
+  Frags<C> Fa, Fb;
+  uint32_t xa[C::FM], wa[C::FN], xb[C::FM], wb[C::FN];
+  read_stage_xd<C>(smem, smem + C::WOFF, smem + C::SOFF, 0, 0, Fa, xa, wa);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  finish_scales<C>(xa, wa, s0, lo, hi);
+  const int n = s1 - s0;
+  const int nr = n < 6 ? 6 : (n + 1) & ~1;
+  ring_stage_xd<C, ZSTART>(smem, X, W, ssr, P, s0, 0, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+#pragma nounroll
+  for (int r = 1; r < nr - 3; r += 2) {
+    ring_stage_xd<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    ring_stage_xd<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+  }
+  ring_stage_xd<C, false, kXdNoCopy1>(smem, X, W, ssr, P, s0, nr - 3, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+  ring_stage_xd<C, false, kXdNoCopy0>(smem, X, W, ssr, P, s0, nr - 2, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+  ring_stage_xd<C, false, kXdLast>(smem, X, W, ssr, P, s0, nr - 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+  MXGG_WAIT_VM(0);
+}
+
 // Reduction over the 64-element stages [s0, s1) restricted to the element
 // range [lo, hi) (chunks and scale blocks outside it are zero / neutral),
 // into acc.  ZSTART: the first stage's MFMAs start from zero, so acc needs no
@@ -653,54 +869,58 @@ template <class C, bool ZSTART = true>
 __device__ __forceinline__ void ring_mainloop(uint8_t* smem, const Operand& X, const Operand& W,
                                               const ScaleSrc& xss, const ScaleSrc& wss, int s0, int s1,
                                               int lo, int hi, v16f (&acc)[C::FM][C::FN]) {
-  if (s0 >= s1) s1 = s0 + 1;
-  s0 &= ~1;
-  Plan<C> P;
-  make_plan<C>(P, X, W, xss, wss);
-  // the scale buffer this wave copies from (wave-uniform)
-  const __amdgpu_buffer_rsrc_t ssr = wave_id() < (C::PS ? C::NXW : C::NSX) ? xss.rsrc : wss.rsrc;
-  // scale groups 0 and 1, then stages s0 .. s0+NS-1 (scales first: every
-  // wait for a stage's copies then covers the scale copies issued before it)
-  const int g0 = C::PS ? (s0 & (C::GSTAGES - 1)) : 0;
-  const int tb = (s0 - g0) / 2;
-  issue_scales<C>(smem + C::SOFF, ssr, P, tb, true);
-  issue_scales<C>(smem + C::SOFF + C::SSLOT, ssr, P, tb + C::GSTEPS, true);
-#pragma unroll
-  for (int i = 0; i < C::NS; ++i) issue_stage<C>(smem + i * C::STAGE, X, W, P, s0 + i, lo, hi);
-  MXGG_WAIT_VM((C::NS - 1) * C::LPS);
-  MXGG_BARRIER();
-  Frags<C> Fa, Fb;
-  uint32_t xa[C::FM], wa[C::FN], xb[C::FM], wb[C::FN];
-  read_stage<C>(smem, smem + C::SOFF, g0 / 2, Fa, xa, wa);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  finish_scales<C>(xa, wa, s0, lo, hi);
-  const int n = s1 - s0;
-  if constexpr (ZSTART) {
-    // stages run: n rounded up to even, at least 6 (those past s1 hold
-    // zeros); the last four start no copies (the prologue and the full
-    // stages already issued every stage of the run), the last reads nothing
-    const int nr = n < 6 ? 6 : (n + 1) & ~1;
-    ring_stage<C, true>(smem, X, W, ssr, P, s0, 0, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-    ring_stage<C>(smem, X, W, ssr, P, s0, 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
-#pragma nounroll
-    for (int r = 2; r < nr - 4; r += 2) {
-      ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-      ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
-    }
-    ring_stage<C, false, kStageNoCopy2>(smem, X, W, ssr, P, s0, nr - 4, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-    ring_stage<C, false, kStageNoCopy1>(smem, X, W, ssr, P, s0, nr - 3, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
-    ring_stage<C, false, kStageNoCopy0>(smem, X, W, ssr, P, s0, nr - 2, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-    ring_stage<C, false, kStageLast>(smem, X, W, ssr, P, s0, nr - 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+  if constexpr (C::XD) {
+    ring_mainloop_xd<C, ZSTART>(smem, X, W, xss, wss, s0, s1, lo, hi, acc);
   } else {
-#pragma nounroll
-    for (int r = 0; r < n; r += 2) {
-      ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
-      ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    if (s0 >= s1) s1 = s0 + 1;
+    s0 &= ~1;
+    Plan<C> P;
+    make_plan<C>(P, X, W, xss, wss);
+    // the scale buffer this wave copies from (wave-uniform)
+    const __amdgpu_buffer_rsrc_t ssr = wave_id() < (C::PS ? C::NXW : C::NSX) ? xss.rsrc : wss.rsrc;
+    // scale groups 0 and 1, then stages s0 .. s0+NS-1 (scales first: every
+    // wait for a stage's copies then covers the scale copies issued before it)
+    const int g0 = C::PS ? (s0 & (C::GSTAGES - 1)) : 0;
+    const int tb = (s0 - g0) / 2;
+    issue_scales<C>(smem + C::SOFF, ssr, P, tb, true);
+    issue_scales<C>(smem + C::SOFF + C::SSLOT, ssr, P, tb + C::GSTEPS, true);
+  #pragma unroll
+    for (int i = 0; i < C::NS; ++i) issue_stage<C>(smem + i * C::STAGE, X, W, P, s0 + i, lo, hi);
+    MXGG_WAIT_VM((C::NS - 1) * C::LPS);
+    MXGG_BARRIER();
+    Frags<C> Fa, Fb;
+    uint32_t xa[C::FM], wa[C::FN], xb[C::FM], wb[C::FN];
+    read_stage<C>(smem, smem + C::SOFF, g0 / 2, Fa, xa, wa);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    finish_scales<C>(xa, wa, s0, lo, hi);
+    const int n = s1 - s0;
+    if constexpr (ZSTART) {
+      // stages run: n rounded up to even, at least 6 (those past s1 hold
+      // zeros); the last four start no copies (the prologue and the full
+      // stages already issued every stage of the run), the last reads nothing
+      const int nr = n < 6 ? 6 : (n + 1) & ~1;
+      ring_stage<C, true>(smem, X, W, ssr, P, s0, 0, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+      ring_stage<C>(smem, X, W, ssr, P, s0, 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+  #pragma nounroll
+      for (int r = 2; r < nr - 4; r += 2) {
+        ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+        ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+      }
+      ring_stage<C, false, kStageNoCopy2>(smem, X, W, ssr, P, s0, nr - 4, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+      ring_stage<C, false, kStageNoCopy1>(smem, X, W, ssr, P, s0, nr - 3, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+      ring_stage<C, false, kStageNoCopy0>(smem, X, W, ssr, P, s0, nr - 2, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+      ring_stage<C, false, kStageLast>(smem, X, W, ssr, P, s0, nr - 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+    } else {
+  #pragma nounroll
+      for (int r = 0; r < n; r += 2) {
+        ring_stage<C>(smem, X, W, ssr, P, s0, r, lo, hi, Fa, xa, wa, Fb, xb, wb, acc);
+        ring_stage<C>(smem, X, W, ssr, P, s0, r + 1, lo, hi, Fb, xb, wb, Fa, xa, wa, acc);
+      }
     }
+    // copies past the last stage (zero fills, scale groups) may still be
+    // writing LDS: drain them before the LDS is reused or released
+    MXGG_WAIT_VM(0);
   }
-  // copies past the last stage (zero fills, scale groups) may still be
-  // writing LDS: drain them before the LDS is reused or released
-  MXGG_WAIT_VM(0);
 }
 
 // The in-range elements of the 16-element chunk at cs (a multiple of 16)
@@ -1886,11 +2106,13 @@ typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 4> CfgF4_256;
 typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 4, true> CfgF8_256P;
 typedef Cfg<128, 128, 2, 2, MXGG_FMT_E4M3, 4, true> CfgF8_128P;
 typedef Cfg<256, 256, 2, 2, MXGG_FMT_E2M1, 4, true> CfgF4_256P;
+// 256 x 256 e4m3 tiles with X in two-stage slots, for row-major X (XLine)
+typedef XLine<Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 3>> CfgF8_256X;
 
 // The scale-independent kernels of a configuration (the reduce): its
 // step-major twin.
 template <class C>
-using StepCfg = Cfg<C::BM, C::BN, C::WGM, C::WGN, C::WFMT, C::NS>;
+using StepCfg = Cfg<C::BM, C::BN, C::WGM, C::WGN, C::WFMT, C::XD ? 4 : C::NS>;
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -2029,7 +2251,8 @@ int launch_fwd(const FwdParams& p0, int grid_m_ub, int gm, int xcd, size_t part_
   // quarter tiles (quad_dp).  The device decides from the real tile count;
   // the host, from the usual one, only skips the launch where it cannot help.
   p.quads = 0;
-  constexpr bool kQuads = std::is_same<C, CfgF8_256>::value || std::is_same<C, CfgF8_256P>::value;
+  constexpr bool kQuads = std::is_same<C, CfgF8_256>::value || std::is_same<C, CfgF8_256P>::value ||
+                          std::is_same<C, CfgF8_256X>::value;
   typedef typename std::conditional<C::PS, CfgF8_128P, CfgF8_128>::type Q;
   if constexpr (kQuads) {
     if (nsteps < kMinSplitTotal && p.par > 0) {
@@ -2372,6 +2595,7 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
     return launch_fwd<CfgF8_128P>(p, gm128, c.group_m, c.xcd, pb, st);
   }
   if (b_fmt == MXGG_FMT_E2M1) return launch_fwd<CfgF4_256>(p, gm256, c.group_m, c.xcd, pb, st);
+  if (c.bm == 256 && p.a_pl == 0) return launch_fwd<CfgF8_256X>(p, gm256, c.group_m, c.xcd, pb, st);
   if (c.bm == 256) return launch_fwd<CfgF8_256>(p, gm256, c.group_m, c.xcd, pb, st);
   return launch_fwd<CfgF8_128>(p, gm128, c.group_m, c.xcd, pb, st);
 }
