@@ -2086,12 +2086,6 @@ static size_t fwd_staging_bytes_a(int64_t M, int64_t N, int64_t K, int b_fmt) {
   return (size_t)M * (size_t)staged_ld(K) + 256;
 }
 
-// Operand layout (MXGG_A_PAIRS / MXGG_B_PAIRS) of a plain-scale forward call
-// given the workspace for its staging (mxgg_grouped_mm_staging_size).
-static int dropin_layout(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
-  return (fwd_staging_bytes(E, M, N, K, b_fmt) ? MXGG_B_PAIRS : 0) | (fwd_staging_bytes_a(M, N, K, b_fmt) ? MXGG_A_PAIRS : 0);
-}
-
 namespace {
 
 typedef Cfg<256, 256, 2, 2, MXGG_FMT_E4M3, 4> CfgF8_256;
@@ -2136,18 +2130,6 @@ const TunedFwd* find_tuned(int E, int64_t M, int64_t N, int64_t K, int b_fmt) {
   return nullptr;
 }
 
-// Whether a tuned entry's tile order (GROUP_M, XCD swizzle) applies to a
-// call on operand layout `layout`: only on the layout the sweep timed --
-// that of the drop-in call at the swept shape, with its operands staged by
-// the library's rule (dropin_layout) -- since the best order differs between
-// layouts.  Its tile shape and split flag apply on every layout: the order
-// never changes the output bits, while the tile shape (through the split
-// plan) and the split can, and calls on different operand layouts give the
-// same bits.
-bool tuned_order_applies(const TunedFwd* t, int layout) {
-  return layout == dropin_layout(t->E, t->M, t->N, t->K, t->b_fmt);
-}
-
 // A tuned entry when the sweep covered the shape.  Otherwise 256 x 256
 // tiles, the 8-XCD swizzle and expert-aligned bands of at most 12 m-blocks
 // (route_tile; 12 beat 8 and 16 on the sweep's jagged groups, and the
@@ -2160,17 +2142,16 @@ bool tuned_order_applies(const TunedFwd* t, int layout) {
 template <class C>
 int fwd_resident();
 
-FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int layout, int bm, int bn, int gm,
-                   int xcd) {
+// A tuned entry applies whole on every operand layout, although the sweep
+// timed the drop-in call's (operands staged by the library's rule): calls on
+// different layouts give the same bits, and the tile order can change them --
+// the tiles of a split last round are the last ones in that order.
+FwdChoice pick_fwd(int E, int64_t M, int64_t N, int64_t K, int b_fmt, int bm, int bn, int gm, int xcd) {
   FwdChoice c{256, 256, 12, 8, true};
   const int64_t tiles256 = (cdiv(M, 256) + E - 1) * cdiv(N, 256);
   const TunedFwd* t = find_tuned(E, M, N, K, b_fmt);
   if (t) {
-    c = FwdChoice{t->bm, t->bn, c.group_m, c.xcd, t->split != 0};
-    if (tuned_order_applies(t, layout)) {
-      c.group_m = t->group_m;
-      c.xcd = t->xcd;
-    }
+    c = FwdChoice{t->bm, t->bn, t->group_m, t->xcd, t->split != 0};
   } else if (b_fmt == MXGG_FMT_E4M3 && tiles256 < 128) {
     // Under half a chip of 256 x 256 tiles: 128 x 128 tiles (two per CU)
     // spread the work over 4x the workgroups, unless the 256 x 256 launch
@@ -2570,7 +2551,7 @@ static int launch_grouped_mm(const uint8_t* A, int64_t lda, const uint8_t* as, c
                              int64_t N, int64_t K, void* out, int out_dtype, int64_t ldo, int block_m, int block_n,
                              int group_m, int xcd, int layout, void* part_area, size_t part_bytes, hipStream_t st,
                              bool plain = false, int64_t ldas = 0, int64_t ldbs_n = 0, int64_t ldbs_e = 0) {
-  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, layout, block_m, block_n, group_m, xcd);
+  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, block_m, block_n, group_m, xcd);
   const bool built = b_fmt == MXGG_FMT_E2M1 ? (c.bm == 256 && c.bn == 256)
                                            : ((c.bm == 256 && c.bn == 256) || (c.bm == 128 && c.bn == 128));
   if (!built) return fail(MXGG_ERR_UNSUPPORTED, "grouped_mm: tile %dx%d not built", c.bm, c.bn);
@@ -2766,7 +2747,7 @@ extern "C" int mxgg_grouped_mm_config(int E, int64_t M, int64_t N, int64_t K, in
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_config: null output pointer");
   if (b_fmt != MXGG_FMT_E4M3 && b_fmt != MXGG_FMT_E2M1)
     return fail(MXGG_ERR_INVALID_ARG, "grouped_mm_config: weight format %d not E4M3/E2M1", b_fmt);
-  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, dropin_layout(E, M, N, K, b_fmt), *block_m, *block_n, *group_m,
+  FwdChoice c = pick_fwd(E, M, N, K, b_fmt, *block_m, *block_n, *group_m,
                          *xcd_swizzle);
   *block_m = c.bm;
   *block_n = c.bn;

@@ -123,9 +123,11 @@ def emit_header(best: dict, source: str = "", min_gain: float | None = None) -> 
         "// `python grouped-gemms_amd/tune_driver.py --emit-header` from the sweep's",
         "// best.json; regenerate rather than edit.  An entry applies to calls with",
         "// the same E, N, K and weight format and M within a factor of two of the",
-        "// swept M; its GROUP_M and XCD swizzle only on the operand layout the sweep",
-        "// timed (the drop-in call's, operands staged by the library's rule at the",
-        "// swept shape).  Fields: E, M, N, K, b_fmt (0 e4m3, 4 e2m1), block_m, block_n,",
+        "// swept M, on every operand layout (the sweep timed the drop-in call's,",
+        "// operands staged by the library's rule at the swept shape; the whole entry",
+        "// applies elsewhere too, since the tile order can change the bits of a call",
+        "// whose last round is split).  Fields: E, M, N, K, b_fmt (0 e4m3, 4 e2m1),",
+        "// block_m, block_n,",
         "// group_m, xcd swizzle, split (1: the last round may be split along K when",
         "// the workspace allows it, 0: whole tiles only).",
         f"// sweep: {source or 'none'}",
