@@ -2415,15 +2415,18 @@ static size_t split_area(int64_t tiles, size_t tile_bytes, int64_t nsteps) {
 
 // Extra workspace for staging both wgrad operands (go_t (N, M), ia_t (K, M))
 // in row pairs, or 0 where that would not pay.  The copy moves 2 (N + K) M
-// bytes in the scale re-layout launch; the GEMM then copies whole lines
-// (kernel-only, row pairs are 19% faster over the sweep).  Measured on the
-// whole drop-in call against the unstaged one (MI355X, M = 16640, 36 sweep
-// shapes, same bits on all): -5.0% geomean, -2 to -15% on every shape but
-// the smallest reductions with few groups (E = 1 with N + K <= 7168, E = 2
-// with N = K = 2048: +1 to +2.4%), which this rule leaves out.
+// bytes in the scale re-layout launch; the GEMM then copies whole lines of
+// both operands, where on row-major data the XLine kernel copies whole lines
+// of go_t only (kernel-only, row pairs are 13% faster over the sweep).  The
+// copy's time over the GEMM's is about 2000 (N + K) / (N K), so it pays only
+// at N = K = 8192; with 8 or more groups, whose token ranges are short, also
+// at N + K >= 10240.  Measured on the whole drop-in call against staging every
+// shape (MI355X, M = 16640, 36 sweep shapes, same bits on all): -2.1%
+// geomean; without any staging -1.6% (the unstaged calls up to 10% faster,
+// E = 8 at N + K >= 10240 and N = K = 8192 1-4% slower).
 static size_t wgrad_staging_bytes(int E, int64_t M, int64_t N, int64_t K) {
   if (E <= 0 || M <= 0 || M % 32 || N <= 0 || K <= 0 || N % 2 || K % 2) return 0;
-  if (N + K < 10240 && (int64_t)E * (N + K) <= 8192) return 0;
+  if (!((N >= 8192 && K >= 8192) || (E >= 8 && N + K >= 10240))) return 0;
   if (M >= (1 << 22) || N / 2 + K / 2 > (1 << 22)) return 0;   // int offsets, launch grid
   return (size_t)(N + K) * (size_t)staged_ld(M) + 512;
 }
@@ -2878,11 +2881,14 @@ static WgradChoice wgrad_choice(int E, int64_t M, int64_t N, int64_t K, int64_t 
 
 // The wgrad launches of a checked call on step-major scales (gs: GO [T][N],
 // is: IA [T][K] dwords); part / part_bytes: room for the fp32 partial tiles
-// of tiles cut along the tokens (none: no tile is cut).
-static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, const uint8_t* ia_t, int64_t ld_ia,
-                        const uint8_t* is, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
-                        int out_dtype, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
-  typedef CfgF8_256 C;
+// of tiles cut along the tokens (none: no tile is cut).  C: the 256 x 256
+// configuration (XLine where GO, the X side, is row-major); the plan, the
+// partial layout and the reduce are the one-stage configuration's, so both
+// give the same bits.
+template <class C>
+static int launch_wgrad_c(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, const uint8_t* ia_t, int64_t ld_ia,
+                          const uint8_t* is, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
+                          int out_dtype, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
   const int64_t T = cdiv(M, STEP);
   // no more room than the split plans of this shape can use (ws_layout)
   const size_t cap = wgrad_part_cap(E, M, N, K);
@@ -2931,9 +2937,19 @@ static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, c
   if (units_ub <= 0) return MXGG_OK;
   hipLaunchKernelGGL((wgrad_kernel<C, true>), dim3((unsigned)units_ub), dim3(C::NT), 0, st, p);
   if (int rc = launch_status("wgrad")) return rc;
-  hipLaunchKernelGGL((wgrad_reduce_kernel<C>), dim3((unsigned)(split_tiles_ub * ReduceShape<C>::CH)), dim3(256),
-                     0, st, p);
+  hipLaunchKernelGGL((wgrad_reduce_kernel<StepCfg<C>>), dim3((unsigned)(split_tiles_ub * ReduceShape<C>::CH)),
+                     dim3(256), 0, st, p);
   return launch_status("wgrad");
+}
+
+static int launch_wgrad(const uint8_t* go_t, int64_t ld_go, const uint8_t* gs, const uint8_t* ia_t, int64_t ld_ia,
+                        const uint8_t* is, const int32_t* offs, int E, int64_t M, int64_t N, int64_t K, void* out,
+                        int out_dtype, int layout, void* part_area, size_t part_bytes, hipStream_t st) {
+  if (layout & MXGG_A_PAIRS)
+    return launch_wgrad_c<CfgF8_256>(go_t, ld_go, gs, ia_t, ld_ia, is, offs, E, M, N, K, out, out_dtype, layout,
+                                     part_area, part_bytes, st);
+  return launch_wgrad_c<CfgF8_256X>(go_t, ld_go, gs, ia_t, ld_ia, is, offs, E, M, N, K, out, out_dtype, layout,
+                                    part_area, part_bytes, st);
 }
 
 extern "C" int mxgg_wgrad_config(int E, int64_t M, int64_t N, int64_t K, int* block) {

@@ -341,9 +341,10 @@ size_t mxgg_wgrad_workspace_size(int E, int64_t M, int64_t N, int64_t K);
 /*
  * Workspace bytes, on top of mxgg_wgrad_workspace_size, with which mxgg_wgrad
  * stages both operands in row pairs ((N + K) * M rounded up to 64, plus 512),
- * or 0 where the copy would not pay for itself: it is left out for N + K <
- * 10240 with E * (N + K) <= 8192 (small reductions in few groups), for odd N
- * or K, and for M not a multiple of 32.  No counterpart in the reference.
+ * or 0 where the copy would not pay for itself: it is offered only for N and
+ * K both at least 8192, or with E >= 8 groups for N + K >= 10240 (elsewhere
+ * the GEMM reads row-major go_t in whole lines, XLine), and never for odd N
+ * or K or for M not a multiple of 32.  No counterpart in the reference.
  */
 size_t mxgg_wgrad_staging_size(int E, int64_t M, int64_t N, int64_t K);
 /*

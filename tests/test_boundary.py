@@ -140,12 +140,14 @@ def test_grouped_mm_workspace_without_gpu():
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8192, E2M1) == 16640 * 8192 + 256   # A only
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 4096, 8192, E2M1) == 0     # an e2m1 weight is not staged
     assert lib.mxgg_grouped_mm_staging_size(1, 16640, 8192, 8200, E4M3) == 0     # K % 32
-    # wgrad: both operands, (N + K) * M rounded up to 64, plus 512; not for N + K < 10240 with
-    # E * (N + K) <= 8192, odd N or K, or M off the 32 grid
-    assert lib.mxgg_wgrad_staging_size(1, 16640, 5120, 5120) == 10240 * 16640 + 512
-    assert lib.mxgg_wgrad_staging_size(2, 2080, 2048, 5120) == 7168 * 2112 + 512
-    assert lib.mxgg_wgrad_staging_size(4, 16640, 2048, 2048) == 4096 * 16640 + 512
-    assert lib.mxgg_wgrad_staging_size(1, 16640, 2048, 5120) == 0
+    # wgrad: both operands, (N + K) * M rounded up to 64, plus 512; only at N, K >= 8192, or with
+    # E >= 8 at N + K >= 10240; not for odd N or K, or M off the 32 grid
+    assert lib.mxgg_wgrad_staging_size(1, 16640, 8192, 8192) == 16384 * 16640 + 512
+    assert lib.mxgg_wgrad_staging_size(8, 2080, 5120, 5120) == 10240 * 2112 + 512
+    assert lib.mxgg_wgrad_staging_size(8, 16640, 2048, 8192) == 10240 * 16640 + 512
+    assert lib.mxgg_wgrad_staging_size(1, 16640, 5120, 5120) == 0
+    assert lib.mxgg_wgrad_staging_size(4, 16640, 8192, 5120) == 0
+    assert lib.mxgg_wgrad_staging_size(8, 16640, 2048, 5120) == 0
     assert lib.mxgg_wgrad_staging_size(2, 16640, 2048, 2048) == 0
     assert lib.mxgg_wgrad_staging_size(1, 16640, 8191, 8192) == 0
     assert lib.mxgg_wgrad_staging_size(1, 16656, 8192, 8192) == 0

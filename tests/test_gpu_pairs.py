@@ -497,9 +497,9 @@ def _pairs_bytes(q, rows, L, dev):
 
 
 @pytest.mark.parametrize("case", [
-    (8, 4096, 768, 640, "odd", torch.bfloat16),        # many small groups, bounds off the 16 grid
-    (2, 2080, 2048, 5120, "even", torch.bfloat16),     # 2080 tokens: rows padded to 2112 when staged
-    (1, 8192, 5120, 5120, "even", torch.float32),      # E = 1, tiles cut along the tokens, f32 out
+    (8, 4096, 2048, 8192, "odd", torch.bfloat16),      # many small groups, bounds off the 16 grid
+    (8, 2080, 5120, 5120, "even", torch.bfloat16),     # 2080 tokens: rows padded to 2112 when staged
+    (1, 8192, 8192, 8192, "even", torch.float32),      # E = 1, tiles cut along the tokens, f32 out
 ], ids=lambda c: "E{}_M{}_N{}_K{}_{}".format(*c[:5]))
 def test_wgrad_staged_operands_bitwise(gpu, case):
     """mxgg_wgrad given mxgg_wgrad_staging_size more workspace copies go_t
