@@ -112,16 +112,20 @@ XLINE_KERNEL = "mxgg::fwd_kernel<mxgg::XLine<mxgg::Cfg<256, 256, 2, 2, 0, 3, fal
 
 # whole-tile kernels with the bf16 epilogue (template argument 1): the bench's outputs are bf16 with aligned rows
 WGRAD_KERNEL = "mxgg::wgrad_kernel<mxgg::Cfg<256, 256, 2, 2, 0, 4, false>, false, 1>"
+WGRAD_XLINE = "mxgg::wgrad_kernel<mxgg::XLine<mxgg::Cfg<256, 256, 2, 2, 0, 3, false> >, false, 1>"
 
 
-def wgrad_kernel_name(E: int, M: int, N: int, K: int) -> str:
+def wgrad_kernel_name(E: int, M: int, N: int, K: int, rows: bool = False) -> str:
     """Device-kernel name of the whole-tile kernel of a wgrad call of this
     shape: 256 x 256 (WGRAD_KERNEL) or, where the library picks them
-    (mxgg_wgrad_config, needs the GPU), 128 x 128 tiles."""
+    (mxgg_wgrad_config, needs the GPU), 128 x 128 tiles; with ``rows``
+    (row-major go_t) the 256 x 256 tiles run as XLine (WGRAD_XLINE)."""
     import ctypes
     from kernels import _lib
     b = ctypes.c_int32(0)
     _lib.check(_lib.load().mxgg_wgrad_config(E, M, N, K, ctypes.byref(b)))
+    if rows and b.value == 256:
+        return WGRAD_XLINE
     return f"mxgg::wgrad_kernel<mxgg::Cfg<{b.value}, {b.value}, 2, 2, 0, 4, false>, false, 1>"
 
 
@@ -518,14 +522,16 @@ def stats_summary(stats_csv: str, bench_json: str, trace_csv: str = None) -> str
         for name, v in sorted(spans.items()):
             out.append(f"  {name:62s} calls {len(v):6d}: re-layout avg {sum(x[0] for x in v) / len(v) / 1e3:8.2f} us, "
                        f"GEMM span avg {sum(x[1] for x in v) / len(v) / 1e3:9.2f} us")
-        # the kernel-only sweep's forward + dgrad calls all run the dominant
-        # kernel; their drop-in twins run it or, where the call stages A in row
-        # pairs, the one-stage 256 x 256 kernel: both, in trace order
-        for key in (rf["kernel"], WGRAD_KERNEL):
-            fam = (FWD_KERNEL, XLINE_KERNEL) if canon(key) in (canon(FWD_KERNEL), canon(XLINE_KERNEL)) else (key,)
-            v = sorted((x for k, xs in spans.items() if canon(k) in {canon(f) for f in fam} for x in xs),
-                       key=lambda x: x[2])
-            bk = rf["by_kernel"].get(key)
+        # the kernel-only sweep's row-major forward + dgrad calls all run the
+        # XLine kernel, their drop-in twins it or, where the call stages A in
+        # row pairs, the one-stage 256 x 256 kernel; the wgrad's likewise (the
+        # one-stage kernel where the call stages both operands): each family's
+        # calls in trace order
+        for fam in ((FWD_KERNEL, XLINE_KERNEL), (WGRAD_KERNEL, WGRAD_XLINE)):
+            names = {canon(f) for f in fam}
+            v = sorted((x for k, xs in spans.items() if canon(k) in names for x in xs), key=lambda x: x[2])
+            key = next((k for k in rf["by_kernel"] if canon(k) in names), None)
+            bk = rf["by_kernel"].get(key) if key else None
             if not bk or len(v) < bk["launches"]:
                 continue
             nb = bk["launches"]
@@ -1089,7 +1095,7 @@ def main():
                 row["wgrad_us"] = med * 1e3
                 row["wgrad_tflops"] = flops / (med * 1e-3) / 1e12
             kernel_only("wgrad_kernel_us", lambda: triton_mxfp8_wgrad(qg, tg, qi, ti, offs),
-                        wgrad_kernel_name(E, M, N, K), flops, row)
+                        wgrad_kernel_name(E, M, N, K, rows=True), flops, row)
             del qg, qi, sg, si, tg, ti
         torch.cuda.empty_cache()
         rows.append(row)

@@ -75,3 +75,14 @@ def test_summary_lines_parse(tmp_path, monkeypatch):
     assert d is not None and d["calls"] == 4320 and d["frac"] == 0.435 and d["frac_with_relayout"] == 0.413
     assert bench.read_dropin_gemm(fw)["kernels"] == [fw, xl]
     assert bench.read_dropin_gemm(bench.WGRAD_KERNEL) is None
+    # the wgrad family's line: the one-stage kernel where the call stages both
+    # operands, XLine on row-major go_t
+    wk, wx = bench.WGRAD_KERNEL, bench.WGRAD_XLINE
+    assert bench.canon(wx) == bench.canon(
+        "void mxgg::wgrad_kernel<mxgg::XLine<mxgg::Cfg<256, 256, 2, 2, 0, 3, false> >, false, 1>(mxgg::WgradParams)")
+    with open(prof / "kernel_stats_sweep.txt", "a") as f:
+        f.write(f"  the sweep's 2100 drop-in calls of {wk} and {wx}: GEMM launches 300.00 us = 2000.0 TFLOP/s = "
+                f"0.400 of 5000.0 (dense MXFP8); with the re-layout launch (20.00 us) 1875.0 TFLOP/s = 0.375\n")
+    w = bench.read_dropin_gemm(wx)
+    assert w is not None and w["calls"] == 2100 and w["kernels"] == [wk, wx] and w["frac_with_relayout"] == 0.375
+    assert bench.read_dropin_gemm(xl)["calls"] == 4320
