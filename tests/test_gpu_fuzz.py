@@ -13,7 +13,9 @@ GEMM itself), any multiple of 32 otherwise (re-laid scales).  wgrad: group
 bounds off the 32-token grid, empty groups, ragged N and K
 (operands from the fused transposing quantizer where their rows allow it,
 else from to_mx of the transposed copy, as the reference quantizes them).
-Sizes keep the fp64 oracle near a second per case.
+Sizes keep the fp64 oracle near a second per case.  Row-major against row
+pairs: the XLine main loop and the one-stage one give the same bits on random
+256 x 256 launches (no oracle needed: the two layouts are the same numbers).
 """
 
 import random
@@ -119,3 +121,45 @@ def test_wgrad_fuzz(gpu, case):
     want = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.astype(np.float32)))
     if np.abs(want).sum():
         assert O.rel_fro(want.astype(np.float64), o) <= REL_FRO_TIGHT
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_row_major_matches_row_pairs_fuzz(gpu, case):
+    """256 x 256 tiles on random shapes: row-major operands (the XLine main
+    loop, the X operand in two-stage LDS slots) give, bit for bit, the
+    one-stage kernel's result on the same operands in row pairs, for the
+    forward and the wgrad (odd stage counts, ragged groups, split calls)."""
+    import kernels
+    rng = random.Random(9100 + case)
+    E = rng.choice([1, 1, 2, 3, 4, 8])
+    M = 2 * rng.randrange(64, 4096)
+    N = 8 * rng.randrange(16, 384)
+    K = 32 * rng.randrange(4, 160)
+    offs = _ends(rng, E, M, 1, cover=rng.random() < 0.75)
+    Mw = 32 * max(1, M // 32)
+    offs_w = _ends(rng, E, Mw, 1, cover=True)
+    print(f"rows/pairs fuzz case {case}: E={E} M={M} N={N} K={K} offs={offs} wgrad M={Mw} offs={offs_w}",
+          flush=True)
+    lay = {"scale_layout": "steps", "data_layout": "pairs"}
+    a = randn_bf16((M, K), 1.0, 500 + case).to(gpu)
+    w = randn_bf16((E, N, K), 0.05, 600 + case).to(gpu)
+    sa, qa = kernels.to_mx(a, scale_layout="steps")
+    sw, qw = kernels.to_mx(w, scale_layout="steps")
+    _, pa = kernels.to_mx(a, **lay)
+    _, pw = kernels.to_mx(w, **lay)
+    o = torch.tensor(offs, dtype=torch.int32, device=gpu)
+    rows = offs[-1]
+    kw = {"BLOCK_M": 256, "BLOCK_N": 256}
+    got = kernels.triton_mxfp8_grouped_mm(qa, qw, sa, sw, o, **kw)[:rows]
+    ref = kernels.triton_mxfp8_grouped_mm(pa, pw, sa, sw, o, **kw)[:rows]
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), "forward"
+    go = randn_bf16((Mw, N), 1.0, 700 + case).to(gpu)
+    ia = randn_bf16((Mw, K), 1.0, 800 + case).to(gpu)
+    sg, qg = kernels.to_mx_dim0(go, scale_layout="steps")
+    si, qi = kernels.to_mx_dim0(ia, scale_layout="steps")
+    _, pg = kernels.to_mx_dim0(go, **lay)
+    _, pi = kernels.to_mx_dim0(ia, **lay)
+    ow = torch.tensor(offs_w, dtype=torch.int32, device=gpu)
+    got = kernels.triton_mxfp8_wgrad(qg, sg, qi, si, ow)
+    ref = kernels.triton_mxfp8_wgrad(pg, sg, pi, si, ow)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), "wgrad"
